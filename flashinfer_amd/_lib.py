@@ -1,0 +1,115 @@
+"""ctypes binding of libmi_moe.so (the C ABI in include/mi_moe.h).
+
+The library is loaded after ``import torch`` so that its ``libamdhip64.so.7``
+dependency binds to the HIP runtime torch already loaded (same SONAME):
+stream handles and device pointers from torch are then valid inside it.
+There is no fallback: if the library is missing the import of the operator
+raises with the command that builds it.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+import threading
+
+import torch  # noqa: F401  (must precede the CDLL load, see module docstring)
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "libmi_moe.so")
+
+MI_MOE_OK = 0
+MI_MOE_ERR_INVALID = 1
+MI_MOE_ERR_WORKSPACE = 2
+MI_MOE_ERR_HIP = 3
+MI_MOE_DTYPE_BF16 = 0
+MI_MOE_DTYPE_F32 = 1
+
+EXPORTED = ("mi_moe_workspace_size", "mi_moe_workspace_layout", "mi_moe_run",
+            "mi_moe_run_profiled", "mi_moe_route", "mi_moe_last_error", "mi_moe_version")
+NUM_PHASES = 5
+PHASES = ("route", "sort", "gemm1_swiglu", "gemm2", "combine")
+
+
+class MiMoeArgs(ctypes.Structure):
+    _fields_ = [
+        ("routing_logits", ctypes.c_void_p),
+        ("routing_bias", ctypes.c_void_p),
+        ("hidden_states", ctypes.c_void_p),
+        ("hidden_states_scale", ctypes.c_void_p),
+        ("gemm1_weights", ctypes.c_void_p),
+        ("gemm1_weights_scale", ctypes.c_void_p),
+        ("gemm2_weights", ctypes.c_void_p),
+        ("gemm2_weights_scale", ctypes.c_void_p),
+        ("local_expert_offset", ctypes.c_int64),
+        ("routed_scaling_factor", ctypes.c_float),
+        ("output", ctypes.c_void_p),
+        ("num_tokens", ctypes.c_int64),
+        ("bias_dtype", ctypes.c_int32),
+        ("reserved", ctypes.c_int32),
+        ("workspace", ctypes.c_void_p),
+        ("workspace_bytes", ctypes.c_size_t),
+    ]
+
+
+class MiMoeLayout(ctypes.Structure):
+    _fields_ = [(n, ctypes.c_size_t) for n in
+                ("topk_ids", "topk_w", "expert_off", "sorted_tok", "sorted_w", "tok_slot",
+                 "act", "part", "total")]
+
+
+_lib = None
+_lock = threading.Lock()
+
+
+class MiMoeError(RuntimeError):
+    def __init__(self, code: int, msg: str):
+        super().__init__(f"mi_moe error {code}: {msg}")
+        self.code = code
+
+
+def lib() -> ctypes.CDLL:
+    global _lib
+    if _lib is not None:
+        return _lib
+    with _lock:
+        if _lib is not None:
+            return _lib
+        if not os.path.exists(LIB_PATH):
+            raise RuntimeError(
+                f"{LIB_PATH} is missing: build it with `python -m flashinfer_amd.build` "
+                "(hipcc, gfx950). There is no non-native fallback.")
+        L = ctypes.CDLL(LIB_PATH)
+        L.mi_moe_workspace_size.argtypes = [ctypes.c_int64]
+        L.mi_moe_workspace_size.restype = ctypes.c_size_t
+        L.mi_moe_workspace_layout.argtypes = [ctypes.c_int64, ctypes.POINTER(MiMoeLayout)]
+        L.mi_moe_workspace_layout.restype = ctypes.c_int
+        L.mi_moe_run.argtypes = [ctypes.POINTER(MiMoeArgs), ctypes.c_void_p]
+        L.mi_moe_run.restype = ctypes.c_int
+        L.mi_moe_run_profiled.argtypes = [ctypes.POINTER(MiMoeArgs), ctypes.c_void_p,
+                                          ctypes.POINTER(ctypes.c_void_p), ctypes.c_int32]
+        L.mi_moe_run_profiled.restype = ctypes.c_int
+        L.mi_moe_route.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int32, ctypes.c_int64,
+                                   ctypes.c_float, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p]
+        L.mi_moe_route.restype = ctypes.c_int
+        L.mi_moe_last_error.argtypes = []
+        L.mi_moe_last_error.restype = ctypes.c_char_p
+        L.mi_moe_version.argtypes = []
+        L.mi_moe_version.restype = ctypes.c_char_p
+        _lib = L
+        return L
+
+
+def check(code: int) -> None:
+    if code != MI_MOE_OK:
+        msg = lib().mi_moe_last_error().decode("utf-8", "replace")
+        raise MiMoeError(code, msg)
+
+
+def workspace_size(num_tokens: int) -> int:
+    return int(lib().mi_moe_workspace_size(int(num_tokens)))
+
+
+def workspace_layout(num_tokens: int) -> MiMoeLayout:
+    out = MiMoeLayout()
+    check(lib().mi_moe_workspace_layout(int(num_tokens), ctypes.byref(out)))
+    return out

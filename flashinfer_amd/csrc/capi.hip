@@ -1,0 +1,210 @@
+// extern "C" boundary of the fused MoE (declared in include/mi_moe.h).
+//
+// mi_moe_run replaces solution/triton/kernel.py::run (kernel.py:600-825).
+// Every argument is checked before the first launch, so a bad call enqueues
+// nothing and reports why through mi_moe_last_error(). The call enqueues
+// route -> sort -> GEMM1+SwiGLU -> GEMM2 -> combine on the caller's stream
+// with grids sized from T alone: no device-to-host copy, no host sync
+// (the reference syncs three times, kernel.py:572, :718, :773).
+#include <math.h>
+#include <stdarg.h>
+#include <stdio.h>
+
+#include <string>
+
+#include "../../include/mi_moe.h"
+#include "common.hpp"
+
+using namespace mimoe;
+
+namespace {
+
+thread_local std::string g_last_error;
+
+int fail(int code, const char* fmt, ...) __attribute__((format(printf, 2, 3)));
+int fail(int code, const char* fmt, ...) {
+    char buf[512];
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(buf, sizeof(buf), fmt, ap);
+    va_end(ap);
+    g_last_error = buf;
+    return code;
+}
+
+constexpr int64_t kMaxTokens = 1 << 22;  // keeps every slot index below 2^31
+
+size_t align_up(size_t x) { return (x + 255) & ~(size_t)255; }
+
+mi_moe_layout make_layout(int64_t T) {
+    mi_moe_layout L;
+    const size_t t = (size_t)(T < 0 ? 0 : T);
+    const size_t s_max = 8 * t;
+    size_t o = 0;
+    L.topk_ids = o;   o = align_up(o + t * TOPK * 4);
+    L.topk_w = o;     o = align_up(o + t * TOPK * 4);
+    L.expert_off = o; o = align_up(o + META_INTS * 4);
+    L.sorted_tok = o; o = align_up(o + s_max * 4);
+    L.sorted_w = o;   o = align_up(o + s_max * 4);
+    L.tok_slot = o;   o = align_up(o + t * TOPK * 4);
+    L.act = o;        o = align_up(o + s_max * I * 2);
+    L.part = o;       o = align_up(o + s_max * H * 4);
+    L.total = o;
+    return L;
+}
+
+bool aligned(const void* p, size_t a) { return ((uintptr_t)p % a) == 0; }
+
+// Kernel variants by token count (weights stream once per row tile).
+int pick_variant(int64_t T) {
+    if (T <= 128) return 0;
+    if (T <= 1024) return 1;
+    return 2;
+}
+
+}  // namespace
+
+extern "C" {
+
+size_t mi_moe_workspace_size(int64_t num_tokens) { return make_layout(num_tokens).total; }
+
+int mi_moe_workspace_layout(int64_t num_tokens, mi_moe_layout* out) {
+    if (!out) return fail(MI_MOE_ERR_INVALID, "mi_moe_workspace_layout: out is NULL");
+    if (num_tokens < 0 || num_tokens > kMaxTokens)
+        return fail(MI_MOE_ERR_INVALID, "mi_moe_workspace_layout: num_tokens %lld out of range",
+                    (long long)num_tokens);
+    *out = make_layout(num_tokens);
+    return MI_MOE_OK;
+}
+
+const char* mi_moe_last_error(void) { return g_last_error.c_str(); }
+
+const char* mi_moe_version(void) { return "mi_moe 0.1.0 gfx950"; }
+
+int mi_moe_route(const float* routing_logits, const void* routing_bias, int32_t bias_dtype,
+                 int64_t num_tokens, float routed_scaling_factor, int32_t* topk_ids,
+                 float* topk_weights, void* stream) {
+    g_last_error.clear();
+    if (num_tokens < 0 || num_tokens > kMaxTokens)
+        return fail(MI_MOE_ERR_INVALID, "mi_moe_route: num_tokens %lld out of range",
+                    (long long)num_tokens);
+    if (bias_dtype != MI_MOE_DTYPE_BF16 && bias_dtype != MI_MOE_DTYPE_F32)
+        return fail(MI_MOE_ERR_INVALID, "mi_moe_route: unknown bias_dtype %d", bias_dtype);
+    if (!isfinite(routed_scaling_factor))
+        return fail(MI_MOE_ERR_INVALID, "mi_moe_route: routed_scaling_factor is not finite");
+    if (num_tokens == 0) return MI_MOE_OK;
+    if (!routing_logits || !routing_bias || !topk_ids || !topk_weights)
+        return fail(MI_MOE_ERR_INVALID, "mi_moe_route: NULL pointer argument");
+    if (!aligned(routing_logits, 16) || !aligned(routing_bias, bias_dtype ? 16 : 8) ||
+        !aligned(topk_ids, 16) || !aligned(topk_weights, 16))
+        return fail(MI_MOE_ERR_INVALID, "mi_moe_route: misaligned pointer");
+    hipError_t err = launch_route(routing_logits, routing_bias, bias_dtype == MI_MOE_DTYPE_F32,
+                                  (int)num_tokens, routed_scaling_factor, topk_ids, topk_weights,
+                                  (hipStream_t)stream);
+    if (err != hipSuccess)
+        return fail(MI_MOE_ERR_HIP, "mi_moe_route: launch failed: %s", hipGetErrorString(err));
+    return MI_MOE_OK;
+}
+
+static int run_impl(const mi_moe_args* a, hipStream_t s, hipEvent_t const* ev) {
+    g_last_error.clear();
+    if (!a) return fail(MI_MOE_ERR_INVALID, "mi_moe_run: args is NULL");
+    const int64_t T = a->num_tokens;
+    if (T < 0 || T > kMaxTokens)
+        return fail(MI_MOE_ERR_INVALID, "mi_moe_run: num_tokens %lld out of range [0, %lld]",
+                    (long long)T, (long long)kMaxTokens);
+    if (a->bias_dtype != MI_MOE_DTYPE_BF16 && a->bias_dtype != MI_MOE_DTYPE_F32)
+        return fail(MI_MOE_ERR_INVALID, "mi_moe_run: unknown bias_dtype %d", a->bias_dtype);
+    if (a->reserved != 0) return fail(MI_MOE_ERR_INVALID, "mi_moe_run: reserved must be 0");
+    if (!isfinite(a->routed_scaling_factor))
+        return fail(MI_MOE_ERR_INVALID, "mi_moe_run: routed_scaling_factor is not finite");
+    if (T == 0) {
+        if (ev) {
+            for (int i = 0; i <= MI_MOE_NUM_PHASES; ++i) {
+                hipError_t e = hipEventRecord(ev[i], s);
+                if (e != hipSuccess)
+                    return fail(MI_MOE_ERR_HIP, "mi_moe_run: event record failed: %s",
+                                hipGetErrorString(e));
+            }
+        }
+        return MI_MOE_OK;
+    }
+
+    const void* ptrs[] = {a->routing_logits, a->routing_bias, a->hidden_states,
+                          a->hidden_states_scale, a->gemm1_weights, a->gemm1_weights_scale,
+                          a->gemm2_weights, a->gemm2_weights_scale, a->output, a->workspace};
+    const char* names[] = {"routing_logits", "routing_bias", "hidden_states",
+                           "hidden_states_scale", "gemm1_weights", "gemm1_weights_scale",
+                           "gemm2_weights", "gemm2_weights_scale", "output", "workspace"};
+    const size_t align[] = {16, (size_t)(a->bias_dtype == MI_MOE_DTYPE_F32 ? 16 : 8), 16, 4, 16,
+                            4, 16, 4, 8, 256};
+    for (int i = 0; i < 10; ++i) {
+        if (!ptrs[i]) return fail(MI_MOE_ERR_INVALID, "mi_moe_run: %s is NULL", names[i]);
+        if (!aligned(ptrs[i], align[i]))
+            return fail(MI_MOE_ERR_INVALID, "mi_moe_run: %s is not %zu-byte aligned", names[i],
+                        align[i]);
+    }
+    const mi_moe_layout L = make_layout(T);
+    if (a->workspace_bytes < L.total)
+        return fail(MI_MOE_ERR_WORKSPACE, "mi_moe_run: workspace has %zu bytes, needs %zu",
+                    a->workspace_bytes, L.total);
+
+    // Offsets outside [-2^30, 2^30] select no expert; clamp so int math stays exact.
+    int64_t off = a->local_expert_offset;
+    if (off > (1 << 30)) off = 1 << 30;
+    if (off < -(1 << 30)) off = -(1 << 30);
+
+    uint8_t* ws = (uint8_t*)a->workspace;
+    Plan p;
+    p.T = (int)T;
+    p.local_offset = (int)off;
+    p.rsf = a->routed_scaling_factor;
+    p.topk_ids = (int*)(ws + L.topk_ids);
+    p.topk_w = (float*)(ws + L.topk_w);
+    p.meta = (int*)(ws + L.expert_off);
+    p.sorted_tok = (int*)(ws + L.sorted_tok);
+    p.sorted_w = (float*)(ws + L.sorted_w);
+    p.tok_slot = (int*)(ws + L.tok_slot);
+    p.act = (uint16_t*)(ws + L.act);
+    p.part = (float*)(ws + L.part);
+
+    const int variant = pick_variant(T);
+    hipError_t err = hipSuccess;
+    auto mark = [&](int i) {
+        if (ev && err == hipSuccess) err = hipEventRecord(ev[i], s);
+    };
+    mark(0);
+    if (err == hipSuccess)
+        err = launch_route(a->routing_logits, a->routing_bias, a->bias_dtype == MI_MOE_DTYPE_F32,
+                           p.T, p.rsf, p.topk_ids, p.topk_w, s);
+    mark(1);
+    if (err == hipSuccess) err = launch_sort(p, gemm1_bm(variant), gemm2_bm(variant), s);
+    mark(2);
+    if (err == hipSuccess)
+        err = launch_gemm1(p, a->hidden_states, a->hidden_states_scale, a->gemm1_weights,
+                           a->gemm1_weights_scale, variant, s);
+    mark(3);
+    if (err == hipSuccess) err = launch_gemm2(p, a->gemm2_weights, a->gemm2_weights_scale, variant, s);
+    mark(4);
+    if (err == hipSuccess) err = launch_combine(p, (uint16_t*)a->output, s);
+    mark(5);
+    if (err != hipSuccess)
+        return fail(MI_MOE_ERR_HIP, "mi_moe_run: launch failed: %s", hipGetErrorString(err));
+    return MI_MOE_OK;
+}
+
+int mi_moe_run(const mi_moe_args* a, void* stream) {
+    return run_impl(a, (hipStream_t)stream, nullptr);
+}
+
+int mi_moe_run_profiled(const mi_moe_args* a, void* stream, void* const* events, int32_t n_events) {
+    g_last_error.clear();
+    if (!events || n_events != MI_MOE_NUM_PHASES + 1)
+        return fail(MI_MOE_ERR_INVALID, "mi_moe_run_profiled: needs %d events, got %d",
+                    MI_MOE_NUM_PHASES + 1, (int)n_events);
+    for (int i = 0; i < n_events; ++i)
+        if (!events[i]) return fail(MI_MOE_ERR_INVALID, "mi_moe_run_profiled: event %d is NULL", i);
+    return run_impl(a, (hipStream_t)stream, (hipEvent_t const*)events);
+}
+
+}  // extern "C"

@@ -1,0 +1,138 @@
+// Shared constants, device helpers and the launch plan of the fused MoE.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stddef.h>
+#include <stdint.h>
+
+namespace mimoe {
+
+// Problem shape of the definition (solution/triton/kernel.py:615-625).
+constexpr int H = 7168;        // hidden size
+constexpr int I = 2048;        // intermediate size
+constexpr int N1 = 2 * I;      // GEMM1 output width (gate | up)
+constexpr int EG = 256;        // global experts
+constexpr int EL = 32;         // local experts per shard
+constexpr int TOPK = 8;
+constexpr int NGROUP = 8;
+constexpr int KGROUP = 4;
+constexpr int GSIZE = EG / NGROUP;  // 32
+constexpr int BLK = 128;            // scale block
+constexpr int HB = H / BLK;         // 56 k-blocks of GEMM1
+constexpr int IB = I / BLK;         // 16 k-blocks of GEMM2
+constexpr int N1B = N1 / BLK;       // 32 n-blocks of GEMM1
+
+// Device pointers into the caller's workspace plus the call's scalars.
+struct Plan {
+    int T;
+    int local_offset;          // clamped into int range by the host
+    float rsf;
+    int* topk_ids;             // [T, 8]
+    float* topk_w;             // [T, 8]
+    int* meta;                 // expert_off[33] | mtile_off1[33] | mtile_off2[33]
+    int* sorted_tok;           // [8T]
+    float* sorted_w;           // [8T]
+    int* tok_slot;             // [T, 8]
+    uint16_t* act;             // bf16 [8T, 2048]
+    float* part;               // [8T, 7168]
+};
+
+constexpr int META_EXPERT_OFF = 0;
+constexpr int META_MTILE1 = 64;
+constexpr int META_MTILE2 = 128;
+constexpr int META_INTS = 192;
+
+typedef int v4i __attribute__((ext_vector_type(4)));
+typedef int v8i __attribute__((ext_vector_type(8)));
+typedef float v4f __attribute__((ext_vector_type(4)));
+typedef __bf16 v8bf __attribute__((ext_vector_type(8)));
+typedef __bf16 v2bf __attribute__((ext_vector_type(2)));
+
+__device__ __forceinline__ uint16_t f2bf(float f) {
+    __bf16 b = (__bf16)f;  // round-to-nearest-even (v_cvt_pk_bf16_f32 on gfx950)
+    return __builtin_bit_cast(uint16_t, b);
+}
+
+__device__ __forceinline__ float bf2f(uint16_t u) {
+    return __builtin_bit_cast(float, (uint32_t)u << 16);
+}
+
+// 16x16x128 fp8(e4m3) x fp8(e4m3) -> fp32, unit block scales (E8M0 127 = 2^0).
+__device__ __forceinline__ v4f mfma_f8_16x16x128(v8i a, v8i b, v4f c) {
+    return __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(a, b, c, 0, 0, 0, 127, 0, 127);
+}
+
+__device__ __forceinline__ v4f mfma_bf16_16x16x32(v8bf a, v8bf b, v4f c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
+}
+
+// Two fp8 e4m3 values (low or high 16 bits of w) -> two bf16, exact.
+template <bool HI>
+__device__ __forceinline__ uint32_t fp8x2_to_bf16x2(uint32_t w) {
+    v2bf r = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w, 1.0f, HI);
+    return __builtin_bit_cast(uint32_t, r);
+}
+
+// Eight fp8 (two dwords) -> eight bf16 (four dwords), exact.
+__device__ __forceinline__ v4i fp8x8_to_bf16x8(uint32_t w0, uint32_t w1) {
+    v4i r;
+    r.x = (int)fp8x2_to_bf16x2<false>(w0);
+    r.y = (int)fp8x2_to_bf16x2<true>(w0);
+    r.z = (int)fp8x2_to_bf16x2<false>(w1);
+    r.w = (int)fp8x2_to_bf16x2<true>(w1);
+    return r;
+}
+
+__device__ __forceinline__ float silu(float x) { return x / (1.0f + __expf(-x)); }
+
+__device__ __forceinline__ int lane_id() { return __lane_id(); }
+
+// Loads 16 bytes through the vector memory path.
+__device__ __forceinline__ v4i ld16(const void* p) { return *reinterpret_cast<const v4i*>(p); }
+
+__device__ __forceinline__ v8i ld_frag(const uint8_t* p) {
+    const v4i lo = ld16(p);
+    const v4i hi = ld16(p + 64);
+    v8i r;
+    r.s0 = lo.x; r.s1 = lo.y; r.s2 = lo.z; r.s3 = lo.w;
+    r.s4 = hi.x; r.s5 = hi.y; r.s6 = hi.z; r.s7 = hi.w;
+    return r;
+}
+
+// Locate the expert and first row of row tile `mt` (prefix table in meta).
+__device__ __forceinline__ bool find_tile(const int* meta, int mtile_base, int mt, int bm, int& e,
+                                          int& row0, int& nrows) {
+    const int total = meta[mtile_base + EL];
+    if (mt >= total) return false;
+    int ee = 0;
+#pragma unroll
+    for (int k = 0; k < EL; ++k) ee += (meta[mtile_base + k + 1] <= mt) ? 1 : 0;
+    e = ee;
+    row0 = meta[META_EXPERT_OFF + ee] + (mt - meta[mtile_base + ee]) * bm;
+    nrows = min(bm, meta[META_EXPERT_OFF + ee + 1] - row0);
+    return true;
+}
+
+// Upper bound on the row tiles of all experts: sum_e ceil(c_e / bm) with
+// sum_e c_e <= 8T and c_e <= T.
+inline int max_mtiles(int T, int bm) {
+    const long long a = (8LL * T + bm - 1) / bm + EL;
+    const long long b = (long long)EL * ((T + bm - 1) / bm);
+    return (int)(a < b ? a : b);
+}
+
+// Host-side launchers (one per kernel family); return hipError_t of the launch.
+hipError_t launch_route(const float* logits, const void* bias, int bias_is_f32, int T, float rsf,
+                        int* topk_ids, float* topk_w, hipStream_t s);
+hipError_t launch_sort(const Plan& p, int bm1, int bm2, hipStream_t s);
+hipError_t launch_gemm1(const Plan& p, const uint8_t* hs, const float* hs_scale, const uint8_t* w1,
+                        const float* w1s, int variant, hipStream_t s);
+hipError_t launch_gemm2(const Plan& p, const uint8_t* w2, const float* w2s, int variant,
+                        hipStream_t s);
+hipError_t launch_combine(const Plan& p, uint16_t* out, hipStream_t s);
+
+// Row-tile height of each GEMM variant (rows of one expert per workgroup).
+int gemm1_bm(int variant);
+int gemm2_bm(int variant);
+
+}  // namespace mimoe

@@ -1,0 +1,146 @@
+// Grouped FP8 GEMM1 (gate | up) with the SwiGLU epilogue fused.
+//
+// Replaces solution/triton/kernel.py:69-186 (_persistent_gemm1_kernel), the
+// input permute at :699-703 and _swiglu_kernel (:301-330):
+//   G[s, n] = sum_kb sa[kb, tok(s)] * sb1[e, n/128, kb] * sum_{k in kb} A8[tok(s), k] * W1[e, n, k]
+//   act[s, j] = silu(G[s, I + j]) * G[s, j]      (SiLU on the second half, :318-326)
+// A rows are gathered straight from hidden_states by the slot's token (no
+// permuted copy). One v_mfma_scale_f32_16x16x128_f8f6f4 covers exactly one
+// 128-wide scale block, so the product of the two block scales is applied
+// to each MFMA result in the fp32 accumulator (kernel.py:168-171).
+//
+// "Stream" variant: weight tiles are not reused across row tiles, so they go
+// global -> VGPR with a D-deep register prefetch ring instead of through LDS.
+// A workgroup is 4 waves; wave w owns gate columns j0..j0+15 and the matching
+// up columns I+j0..I+j0+15 for the BM = 16*MT rows of one expert's row tile.
+//
+// Operand layout: lane l feeds row (l % 16) of a 16x128 operand with bytes
+// [16g, 16g+16) and [64+16g, 64+16g+16) of the 128-byte k-block, g = l / 16.
+// A and B use the same mapping, so the k pairing inside the MFMA is exact
+// whatever order the instruction assigns to the 32 bytes of a lane.
+#include "common.hpp"
+
+namespace mimoe {
+
+template <int MT, int D>
+__global__ __launch_bounds__(256) void gemm1_stream_kernel(Plan p, const uint8_t* __restrict__ hs,
+                                                           const float* __restrict__ hs_scale,
+                                                           const uint8_t* __restrict__ w1,
+                                                           const float* __restrict__ w1s) {
+    static_assert(HB % D == 0, "prefetch depth must divide the k-block count");
+    constexpr int BM = 16 * MT;
+    __shared__ float sa_lds[HB][BM];
+    __shared__ int tok_lds[BM];
+
+    int e, row0, nrows;
+    if (!find_tile(p.meta, META_MTILE1, blockIdx.y, BM, e, row0, nrows)) return;
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    if (tid < BM) tok_lds[tid] = p.sorted_tok[row0 + min(tid, nrows - 1)];
+    __syncthreads();
+    for (int i = tid; i < HB * BM; i += 256) {
+        const int kb = i / BM, m = i % BM;
+        sa_lds[kb][m] = hs_scale[(size_t)kb * p.T + tok_lds[m]];
+    }
+    __syncthreads();
+
+    const int j0 = blockIdx.x * 64 + wave * 16;
+    const int r = lane & 15, g = lane >> 4;
+    const uint8_t* bg_ptr = w1 + ((size_t)e * N1 + j0 + r) * H + g * 16;
+    const uint8_t* bu_ptr = w1 + ((size_t)e * N1 + I + j0 + r) * H + g * 16;
+    const uint8_t* a_ptr[MT];
+#pragma unroll
+    for (int i = 0; i < MT; ++i) a_ptr[i] = hs + (size_t)tok_lds[i * 16 + r] * H + g * 16;
+    const float* sbg_ptr = w1s + ((size_t)e * N1B + j0 / BLK) * HB;
+    const float* sbu_ptr = w1s + ((size_t)e * N1B + (I + j0) / BLK) * HB;
+
+    v8i bg[D], bu[D], a[D][MT];
+    v4f accg[MT], accu[MT];
+    const v4f zero = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int i = 0; i < MT; ++i) { accg[i] = zero; accu[i] = zero; }
+
+    // Consume ring stage d (k-block kb): two MFMAs per row sub-tile, block
+    // scales applied in fp32.
+    auto compute = [&](int d, int kb) __attribute__((always_inline)) {
+        const float sg = sbg_ptr[kb];
+        const float su = sbu_ptr[kb];
+#pragma unroll
+        for (int i = 0; i < MT; ++i) {
+            const v4f pg = mfma_f8_16x16x128(a[d][i], bg[d], zero);
+            const v4f pu = mfma_f8_16x16x128(a[d][i], bu[d], zero);
+            const float4 sa4 = *reinterpret_cast<const float4*>(&sa_lds[kb][i * 16 + g * 4]);
+            accg[i][0] += pg[0] * (sa4.x * sg);
+            accg[i][1] += pg[1] * (sa4.y * sg);
+            accg[i][2] += pg[2] * (sa4.z * sg);
+            accg[i][3] += pg[3] * (sa4.w * sg);
+            accu[i][0] += pu[0] * (sa4.x * su);
+            accu[i][1] += pu[1] * (sa4.y * su);
+            accu[i][2] += pu[2] * (sa4.z * su);
+            accu[i][3] += pu[3] * (sa4.w * su);
+        }
+    };
+    auto load = [&](int d, int kb) __attribute__((always_inline)) {
+        const int nk = kb * BLK;
+        bg[d] = ld_frag(bg_ptr + nk);
+        bu[d] = ld_frag(bu_ptr + nk);
+#pragma unroll
+        for (int i = 0; i < MT; ++i) a[d][i] = ld_frag(a_ptr[i] + nk);
+    };
+
+#pragma unroll
+    for (int d = 0; d < D; ++d) load(d, d);
+
+    // Steady state: every stage is refilled right after it is consumed.
+#pragma unroll 1
+    for (int kb0 = 0; kb0 < HB - D; kb0 += D) {
+#pragma unroll
+        for (int d = 0; d < D; ++d) {
+            compute(d, kb0 + d);
+            load(d, kb0 + d + D);
+        }
+    }
+    // Drain the last D k-blocks.
+#pragma unroll
+    for (int d = 0; d < D; ++d) compute(d, HB - D + d);
+
+#pragma unroll
+    for (int i = 0; i < MT; ++i) {
+#pragma unroll
+        for (int rr = 0; rr < 4; ++rr) {
+            const int m = i * 16 + g * 4 + rr;
+            if (m < nrows) {
+                const float v = silu(accu[i][rr]) * accg[i][rr];
+                p.act[(size_t)(row0 + m) * I + j0 + r] = f2bf(v);
+            }
+        }
+    }
+}
+
+int gemm1_bm(int variant) { return variant == 0 ? 16 : (variant == 1 ? 32 : 64); }
+
+hipError_t launch_gemm1(const Plan& p, const uint8_t* hs, const float* hs_scale, const uint8_t* w1,
+                        const float* w1s, int variant, hipStream_t s) {
+    if (p.T <= 0) return hipSuccess;
+    const int bm = gemm1_bm(variant);
+    dim3 grid(I / 64, max_mtiles(p.T, bm));
+    switch (variant) {
+        case 0:
+            hipLaunchKernelGGL((gemm1_stream_kernel<1, 4>), grid, dim3(256), 0, s, p, hs, hs_scale,
+                               w1, w1s);
+            break;
+        case 1:
+            hipLaunchKernelGGL((gemm1_stream_kernel<2, 4>), grid, dim3(256), 0, s, p, hs, hs_scale,
+                               w1, w1s);
+            break;
+        default:
+            hipLaunchKernelGGL((gemm1_stream_kernel<4, 2>), grid, dim3(256), 0, s, p, hs, hs_scale,
+                               w1, w1s);
+            break;
+    }
+    return hipGetLastError();
+}
+
+}  // namespace mimoe

@@ -1,0 +1,178 @@
+"""Drop-in entry point of the fused MoE: ``run(...)``.
+
+Same signature, argument meaning and destination-passing contract as the
+reference solution ``solution/triton/kernel.py::run`` (kernel.py:600-613,
+config.toml:8): fills ``output`` in place and returns ``None``. Every row of
+``output`` is overwritten; tokens with no local expert get zeros
+(kernel.py:692-695, :801). Scalars may be Python numbers or 0-d tensors
+(``int()``/``float()`` as at kernel.py:547-548).
+
+The work runs in libmi_moe.so on torch's current stream: route, sort,
+GEMM1+SwiGLU, GEMM2 and combine kernels for gfx950, with no host
+synchronisation and no allocation after the first call at a given size
+(the workspace is cached per device and stream).
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+
+import torch
+
+from . import _lib
+
+H, I, E_GLOBAL, E_LOCAL, BLOCK = 7168, 2048, 256, 32, 128
+FP8 = torch.float8_e4m3fn
+
+_workspaces: dict = {}
+
+
+def _workspace(device: torch.device, stream: int, nbytes: int) -> torch.Tensor:
+    key = (device.index, stream)
+    ws = _workspaces.get(key)
+    if ws is None or ws.numel() < nbytes:
+        # round up so a slowly growing T does not reallocate every call
+        size = max(nbytes, 1 << 20)
+        size = 1 << (size - 1).bit_length() if size < (1 << 30) else size
+        ws = torch.empty(size, dtype=torch.uint8, device=device)
+        _workspaces[key] = ws
+    return ws
+
+
+def _expect(t: torch.Tensor, name: str, dtypes, shape) -> None:
+    if not isinstance(t, torch.Tensor):
+        raise TypeError(f"{name} must be a torch.Tensor, got {type(t).__name__}")
+    if t.dtype not in dtypes:
+        raise TypeError(f"{name} must have dtype in {[str(d) for d in dtypes]}, got {t.dtype}")
+    if tuple(t.shape) != tuple(shape):
+        raise ValueError(f"{name} must have shape {tuple(shape)}, got {tuple(t.shape)}")
+
+
+def _scalar(x, kind):
+    if isinstance(x, torch.Tensor):
+        if x.numel() != 1:
+            raise ValueError("scalar arguments must be Python numbers or 1-element tensors")
+        x = x.item()
+    return kind(x)
+
+
+@torch.no_grad()
+def run(
+    routing_logits: torch.Tensor,
+    routing_bias: torch.Tensor,
+    hidden_states: torch.Tensor,
+    hidden_states_scale: torch.Tensor,
+    gemm1_weights: torch.Tensor,
+    gemm1_weights_scale: torch.Tensor,
+    gemm2_weights: torch.Tensor,
+    gemm2_weights_scale: torch.Tensor,
+    local_expert_offset: int,
+    routed_scaling_factor: float,
+    output: torch.Tensor,
+):
+    _call(routing_logits, routing_bias, hidden_states, hidden_states_scale, gemm1_weights,
+          gemm1_weights_scale, gemm2_weights, gemm2_weights_scale, local_expert_offset,
+          routed_scaling_factor, output, None)
+    return None
+
+
+@torch.no_grad()
+def run_profiled(*args, events):
+    """``run`` that also records ``events`` (6 ``torch.cuda.Event`` with
+    timing enabled) around the route, sort, gemm1_swiglu, gemm2 and combine
+    phases, on the stream the kernels run on (kernel.py:634-672 analogue)."""
+    if len(events) != _lib.NUM_PHASES + 1:
+        raise ValueError(f"need {_lib.NUM_PHASES + 1} events")
+    _call(*args, events)
+
+
+def _call(routing_logits, routing_bias, hidden_states, hidden_states_scale, gemm1_weights,
+          gemm1_weights_scale, gemm2_weights, gemm2_weights_scale, local_expert_offset,
+          routed_scaling_factor, output, events):
+    if not isinstance(routing_logits, torch.Tensor) or routing_logits.dim() != 2:
+        raise ValueError("routing_logits must be a 2-D tensor [T, 256]")
+    T = int(routing_logits.shape[0])
+    _expect(routing_logits, "routing_logits", (torch.float32,), (T, E_GLOBAL))
+    _expect(routing_bias, "routing_bias", (torch.bfloat16, torch.float32), (E_GLOBAL,))
+    _expect(hidden_states, "hidden_states", (FP8,), (T, H))
+    _expect(hidden_states_scale, "hidden_states_scale", (torch.float32,), (H // BLOCK, T))
+    _expect(gemm1_weights, "gemm1_weights", (FP8,), (E_LOCAL, 2 * I, H))
+    _expect(gemm1_weights_scale, "gemm1_weights_scale", (torch.float32,),
+            (E_LOCAL, 2 * I // BLOCK, H // BLOCK))
+    _expect(gemm2_weights, "gemm2_weights", (FP8,), (E_LOCAL, H, I))
+    _expect(gemm2_weights_scale, "gemm2_weights_scale", (torch.float32,),
+            (E_LOCAL, H // BLOCK, I // BLOCK))
+    _expect(output, "output", (torch.bfloat16,), (T, H))
+    tensors = (routing_logits, routing_bias, hidden_states, hidden_states_scale, gemm1_weights,
+               gemm1_weights_scale, gemm2_weights, gemm2_weights_scale, output)
+    device = output.device
+    if device.type != "cuda":
+        raise ValueError("run() needs tensors on a ROCm GPU (device type 'cuda'); there is no "
+                         "CPU path")
+    for t in tensors:
+        if t.device != device:
+            raise ValueError("all tensors must be on the same device")
+    offset = _scalar(local_expert_offset, int)
+    rsf = _scalar(routed_scaling_factor, float)
+    if T == 0 and events is None:
+        return
+
+    ins = [t.contiguous() for t in tensors[:-1]]
+    out = output if output.is_contiguous() else torch.empty_like(
+        output, memory_format=torch.contiguous_format)
+    with torch.cuda.device(device):
+        cur = torch.cuda.current_stream(device)
+        stream = cur.cuda_stream
+        need = _lib.workspace_size(T)
+        ws = _workspace(device, stream, need)
+        args = _lib.MiMoeArgs(
+            routing_logits=ins[0].data_ptr(), routing_bias=ins[1].data_ptr(),
+            hidden_states=ins[2].data_ptr(), hidden_states_scale=ins[3].data_ptr(),
+            gemm1_weights=ins[4].data_ptr(), gemm1_weights_scale=ins[5].data_ptr(),
+            gemm2_weights=ins[6].data_ptr(), gemm2_weights_scale=ins[7].data_ptr(),
+            local_expert_offset=offset, routed_scaling_factor=rsf,
+            output=out.data_ptr(), num_tokens=T,
+            bias_dtype=(_lib.MI_MOE_DTYPE_BF16 if ins[1].dtype == torch.bfloat16
+                        else _lib.MI_MOE_DTYPE_F32),
+            reserved=0, workspace=ws.data_ptr(), workspace_bytes=ws.numel())
+        if events is None:
+            _lib.check(_lib.lib().mi_moe_run(ctypes.byref(args), ctypes.c_void_p(stream)))
+        else:
+            handles = []
+            for ev in events:
+                if ev.cuda_event == 0:  # torch creates the HIP event on first record
+                    ev.record(cur)
+                handles.append(ev.cuda_event)
+            arr = (ctypes.c_void_p * len(handles))(*handles)
+            _lib.check(_lib.lib().mi_moe_run_profiled(ctypes.byref(args), ctypes.c_void_p(stream),
+                                                      arr, len(handles)))
+    if out is not output:
+        output.copy_(out)
+
+
+def route(routing_logits: torch.Tensor, routing_bias: torch.Tensor, routed_scaling_factor: float):
+    """Routing only: (global top-8 ids int32 [T,8] in selection order, weights fp32 [T,8])."""
+    T = int(routing_logits.shape[0])
+    _expect(routing_logits, "routing_logits", (torch.float32,), (T, E_GLOBAL))
+    _expect(routing_bias, "routing_bias", (torch.bfloat16, torch.float32), (E_GLOBAL,))
+    dev = routing_logits.device
+    ids = torch.empty(T, 8, dtype=torch.int32, device=dev)
+    w = torch.empty(T, 8, dtype=torch.float32, device=dev)
+    if T == 0:
+        return ids, w
+    lg = routing_logits.contiguous()
+    bs = routing_bias.contiguous()
+    with torch.cuda.device(dev):
+        stream = torch.cuda.current_stream(dev).cuda_stream
+        _lib.check(_lib.lib().mi_moe_route(
+            lg.data_ptr(), bs.data_ptr(),
+            _lib.MI_MOE_DTYPE_BF16 if bs.dtype == torch.bfloat16 else _lib.MI_MOE_DTYPE_F32,
+            T, float(routed_scaling_factor), ids.data_ptr(), w.data_ptr(), ctypes.c_void_p(stream)))
+    return ids, w
+
+
+def last_workspace(device: torch.device | None = None) -> torch.Tensor:
+    """The cached workspace of the current stream (for staged parity checks)."""
+    device = device or torch.device("cuda", torch.cuda.current_device())
+    stream = torch.cuda.current_stream(device).cuda_stream
+    return _workspaces[(device.index, stream)]

@@ -1,0 +1,111 @@
+/*
+ * mi_moe: MI355X (gfx950) fused Mixture-of-Experts operator, C ABI.
+ *
+ * One call computes the DeepSeek-routed, FP8 block-scaled MoE layer for one
+ * expert-parallel shard of 32 local experts, definition
+ * moe_fp8_block_scale_ds_routing_topk8_ng8_kg4_e32_h7168_i2048
+ * (H = 7168, I = 2048, 256 global experts in 8 groups of 32, top-4 groups,
+ * top-8 experts, 128-element scale blocks).
+ *
+ * All pointers are device pointers; the caller owns every buffer, including
+ * the workspace. The library never allocates device memory, never
+ * synchronises the host, and enqueues all work on the given stream.
+ */
+#ifndef MI_MOE_H_
+#define MI_MOE_H_
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Status codes. */
+#define MI_MOE_OK 0
+#define MI_MOE_ERR_INVALID 1   /* bad pointer, size, alignment or scalar */
+#define MI_MOE_ERR_WORKSPACE 2 /* workspace_bytes < mi_moe_workspace_size(T) */
+#define MI_MOE_ERR_HIP 3       /* a HIP launch failed */
+
+/* Element type of routing_bias. */
+#define MI_MOE_DTYPE_BF16 0
+#define MI_MOE_DTYPE_F32 1
+
+/* Arguments of one call. Field order and meaning follow the reference entry
+ * point solution/triton/kernel.py:600-613 (run(routing_logits, routing_bias,
+ * hidden_states, hidden_states_scale, gemm1_weights, gemm1_weights_scale,
+ * gemm2_weights, gemm2_weights_scale, local_expert_offset,
+ * routed_scaling_factor, output)); shapes are those of kernel.py:615-627.
+ * Every tensor is dense, row-major, 16-byte aligned. */
+typedef struct mi_moe_args {
+    const float* routing_logits;       /* fp32 [T, 256] */
+    const void* routing_bias;          /* bf16 or fp32 [256] (bias_dtype) */
+    const uint8_t* hidden_states;      /* fp8 e4m3fn [T, 7168] */
+    const float* hidden_states_scale;  /* fp32 [56, T] (block-major) */
+    const uint8_t* gemm1_weights;      /* fp8 e4m3fn [32, 4096, 7168] */
+    const float* gemm1_weights_scale;  /* fp32 [32, 32, 56] */
+    const uint8_t* gemm2_weights;      /* fp8 e4m3fn [32, 7168, 2048] */
+    const float* gemm2_weights_scale;  /* fp32 [32, 56, 16] */
+    int64_t local_expert_offset;       /* first global expert id of this shard */
+    float routed_scaling_factor;
+    void* output;                      /* bf16 [T, 7168], fully overwritten */
+    int64_t num_tokens;                /* T >= 0 */
+    int32_t bias_dtype;                /* MI_MOE_DTYPE_* */
+    int32_t reserved;                  /* must be 0 */
+    void* workspace;                   /* >= mi_moe_workspace_size(T) bytes, 256-B aligned */
+    size_t workspace_bytes;
+} mi_moe_args;
+
+/* Byte offsets of the intermediate buffers inside the workspace, for staged
+ * parity checks. Layout of each buffer:
+ *   topk_ids   int32 [T, 8]   global expert ids in selection order
+ *   topk_w     fp32  [T, 8]   routing weights (kernel.py:450)
+ *   expert_off int32 [33]     exclusive prefix of local slot counts (S = [32])
+ *   sorted_tok int32 [8T]     token of each slot, expert-major, token-ascending
+ *   sorted_w   fp32  [8T]     routing weight of each slot
+ *   tok_slot   int32 [T, 8]   slots of each token, ascending local expert, -1 pad
+ *   act        bf16  [8T, 2048]  SwiGLU(GEMM1) per slot
+ *   part       fp32  [8T, 7168]  GEMM2 per slot (unweighted)               */
+typedef struct mi_moe_layout {
+    size_t topk_ids, topk_w, expert_off, sorted_tok, sorted_w, tok_slot, act, part;
+    size_t total;
+} mi_moe_layout;
+
+/* Workspace bytes needed for T tokens. Replaces the reference's per-call
+ * torch allocations (kernel.py:535-536, :576-581, :710, :747, :769, :801). */
+size_t mi_moe_workspace_size(int64_t num_tokens);
+
+/* Fills *out with the workspace layout for T tokens. Returns MI_MOE_OK. */
+int mi_moe_workspace_layout(int64_t num_tokens, mi_moe_layout* out);
+
+/* The fused MoE forward pass; replaces kernel.py::run (kernel.py:600-825).
+ * Validates everything before the first launch; on error nothing is
+ * enqueued. stream is a hipStream_t (NULL = default stream). */
+int mi_moe_run(const mi_moe_args* args, void* stream);
+
+/* mi_moe_run plus phase timing: records the caller's HIP events
+ * (hipEvent_t, n_events == MI_MOE_NUM_PHASES + 1) on the stream before the
+ * first kernel and after each of the phases route, sort, gemm1 (+SwiGLU),
+ * gemm2, combine. Counterpart of the reference's env-gated phase events
+ * (kernel.py:634-672, phase names :677-823). */
+#define MI_MOE_NUM_PHASES 5
+int mi_moe_run_profiled(const mi_moe_args* args, void* stream, void* const* events,
+                        int32_t n_events);
+
+/* Routing only (kernel.py:371-457 without the local filter): writes global
+ * top-8 ids (int32 [T, 8], selection order) and weights (fp32 [T, 8]). */
+int mi_moe_route(const float* routing_logits, const void* routing_bias, int32_t bias_dtype,
+                 int64_t num_tokens, float routed_scaling_factor, int32_t* topk_ids,
+                 float* topk_weights, void* stream);
+
+/* Message of the last error on the calling thread ("" if none). */
+const char* mi_moe_last_error(void);
+
+/* Library version string. */
+const char* mi_moe_version(void);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* MI_MOE_H_ */

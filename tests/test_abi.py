@@ -1,0 +1,114 @@
+"""CPU tests of the C ABI: the library loads, exports every function that
+include/mi_moe.h declares, and rejects bad calls before any launch."""
+import ctypes
+import os
+import re
+
+import pytest
+import torch
+
+from flashinfer_amd import _lib, kernel
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+
+
+def _declared_functions():
+    src = open(os.path.join(ROOT, "include", "mi_moe.h")).read()
+    src = re.sub(r"/\*.*?\*/", "", src, flags=re.S)
+    return sorted(set(re.findall(r"\b(mi_moe_[a-z_]+)\s*\(", src)))
+
+
+def test_library_exports_every_declared_symbol():
+    L = _lib.lib()
+    decl = _declared_functions()
+    assert decl, "no declarations parsed"
+    for name in decl:
+        assert hasattr(L, name), f"{name} declared in mi_moe.h but not exported"
+    assert set(decl) == set(_lib.EXPORTED)
+
+
+def test_version():
+    assert b"gfx950" in _lib.lib().mi_moe_version()
+
+
+def test_workspace_layout_monotone_and_aligned():
+    prev = 0
+    for T in (1, 2, 16, 64, 1024, 8192, 14000):
+        L = _lib.workspace_layout(T)
+        offs = [L.topk_ids, L.topk_w, L.expert_off, L.sorted_tok, L.sorted_w, L.tok_slot, L.act, L.part]
+        assert offs == sorted(offs)
+        assert all(o % 256 == 0 for o in offs)
+        assert L.total == _lib.workspace_size(T) and L.total > prev
+        assert L.total - L.part >= 8 * T * 7168 * 4
+        prev = L.total
+
+
+def _args(**over):
+    a = _lib.MiMoeArgs()
+    ptr = 1 << 20  # 256-byte aligned fake addresses: never dereferenced on these paths
+    for f, _ in _lib.MiMoeArgs._fields_:
+        if f in ("local_expert_offset", "num_tokens", "bias_dtype", "reserved", "workspace_bytes"):
+            continue
+        if f == "routed_scaling_factor":
+            continue
+        setattr(a, f, ptr)
+        ptr += 1 << 20
+    a.num_tokens = 16
+    a.routed_scaling_factor = 2.5
+    a.workspace_bytes = 0
+    for k, v in over.items():
+        setattr(a, k, v)
+    return a
+
+
+def _call(a):
+    return _lib.lib().mi_moe_run(ctypes.byref(a), None)
+
+
+def test_run_rejects_before_launch():
+    L = _lib.lib()
+    assert L.mi_moe_run(None, None) == _lib.MI_MOE_ERR_INVALID
+    assert _call(_args(num_tokens=-1)) == _lib.MI_MOE_ERR_INVALID
+    assert b"num_tokens" in L.mi_moe_last_error()
+    assert _call(_args(bias_dtype=7)) == _lib.MI_MOE_ERR_INVALID
+    assert _call(_args(reserved=1)) == _lib.MI_MOE_ERR_INVALID
+    assert _call(_args(routed_scaling_factor=float("nan"))) == _lib.MI_MOE_ERR_INVALID
+    assert _call(_args(gemm2_weights=None)) == _lib.MI_MOE_ERR_INVALID
+    assert b"gemm2_weights is NULL" in L.mi_moe_last_error()
+    assert _call(_args(hidden_states=(1 << 20) + 4)) == _lib.MI_MOE_ERR_INVALID
+    assert b"aligned" in L.mi_moe_last_error()
+    assert _call(_args(workspace_bytes=100)) == _lib.MI_MOE_ERR_WORKSPACE
+    assert b"workspace" in L.mi_moe_last_error()
+    # T == 0 is a valid no-op
+    assert _call(_args(num_tokens=0)) == _lib.MI_MOE_OK
+    assert L.mi_moe_last_error() == b""
+
+
+def test_route_rejects_before_launch():
+    L = _lib.lib()
+    assert L.mi_moe_route(None, None, 0, -1, 2.5, None, None, None) == _lib.MI_MOE_ERR_INVALID
+    assert L.mi_moe_route(None, None, 0, 4, 2.5, None, None, None) == _lib.MI_MOE_ERR_INVALID
+    assert L.mi_moe_route(None, None, 5, 4, 2.5, None, None, None) == _lib.MI_MOE_ERR_INVALID
+    assert L.mi_moe_route(None, None, 0, 0, 2.5, None, None, None) == _lib.MI_MOE_OK
+
+
+def test_python_wrapper_validates_shapes_and_device():
+    T = 4
+    good = dict(
+        routing_logits=torch.zeros(T, 256), routing_bias=torch.zeros(256, dtype=torch.bfloat16),
+        hidden_states=torch.zeros(T, 7168).to(torch.float8_e4m3fn),
+        hidden_states_scale=torch.zeros(56, T),
+        gemm1_weights=torch.empty(32, 4096, 7168, dtype=torch.float8_e4m3fn),
+        gemm1_weights_scale=torch.zeros(32, 32, 56),
+        gemm2_weights=torch.empty(32, 7168, 2048, dtype=torch.float8_e4m3fn),
+        gemm2_weights_scale=torch.zeros(32, 56, 16),
+        local_expert_offset=0, routed_scaling_factor=2.5,
+        output=torch.zeros(T, 7168, dtype=torch.bfloat16))
+    bad = dict(good, hidden_states_scale=torch.zeros(T, 56))
+    with pytest.raises(ValueError, match="hidden_states_scale"):
+        kernel.run(**bad)
+    bad = dict(good, routing_logits=torch.zeros(T, 256, dtype=torch.float64))
+    with pytest.raises(TypeError, match="routing_logits"):
+        kernel.run(**bad)
+    with pytest.raises(ValueError, match="GPU"):
+        kernel.run(**good)

@@ -1,0 +1,194 @@
+"""GPU parity of the fused MoE against the CPU oracle, through the C ABI.
+
+Bars (written in each test):
+* routing: top-8 id SETS bit-exact per token (order is unspecified);
+  weights within 1e-6 relative (same formula, fp32, different sum order);
+* slot order, expert offsets, per-token slot lists: bit-exact;
+* output: |out - ref| <= 1e-2 * |ref| + 1e-2 * max|ref| elementwise against the
+  oracle's fp32 accumulator, no element outside;
+* determinism: two calls are bit-identical.
+"""
+import pytest
+import torch
+
+from flashinfer_amd import workloads as W
+
+from _helpers import log, oracle_subset, run_gpu, spread_tokens, gpu_args
+
+pytestmark = pytest.mark.gpu
+
+RTOL, ATOL_REL = 1e-2, 1e-2
+
+
+@pytest.fixture(scope="module", autouse=True)
+def _need_gpu():
+    if not torch.cuda.is_available():
+        pytest.skip("no GPU")
+    from flashinfer_amd import _lib
+    _lib.lib()
+
+
+def _route_check(wl):
+    from flashinfer_amd import kernel
+    from oracle import ref_moe as R
+    t = wl.tensors
+    ids, w = kernel.route(t["routing_logits"].cuda(), t["routing_bias"].cuda(), wl.routed_scaling_factor)
+    ids, w = ids.cpu(), w.cpu()
+    ref = R.route(t["routing_logits"], t["routing_bias"], wl.routed_scaling_factor)
+    mism = R.routing_set_mismatch(ids, ref.ids)
+    ties = R.near_tie_tokens(t["routing_logits"], t["routing_bias"])
+    log(f"route {wl.name}: T={wl.T} set mismatches={mism} near-tie tokens={ties}")
+    assert mism == 0
+    # same selection order, so weights line up position by position
+    assert torch.equal(ids.long(), ref.ids)
+    assert torch.allclose(w, ref.weights, rtol=1e-6, atol=0)
+
+
+@pytest.mark.parametrize("name", ["c1_t1", "c1_t4", "c0_t16", "c1_t64", "c2_t1024_o0", "c3_t8192",
+                                  "c4_t14000_skew"])
+def test_route_parity(name):
+    log(f"test_route_parity[{name}]")
+    wl = W.standard_tokens(name)
+    _route_check(wl)
+
+
+def _check_output(wl, out, tokens):
+    from oracle import ref_moe as R
+    ref = oracle_subset(wl, tokens)
+    got = out[tokens.to(out.device)].float().cpu()
+    rep = R.tolerance_report(got, ref.acc)
+    n_slots = sum(len(tk) for tk, _ in ref.slots)
+    log(f"output {wl.name}: tokens={len(tokens)} slots={n_slots} {rep}")
+    assert torch.isfinite(got).all()
+    assert rep["n_bad"] == 0, rep
+    return rep
+
+
+@pytest.mark.parametrize("name", ["c1_t1", "c1_t4", "c0_t16", "c1_t16", "c1_t64"])
+def test_output_parity_decode(name):
+    log(f"test_output_parity_decode[{name}]")
+    wl = W.standard(name)
+    out = run_gpu(wl, fill=float("nan"))
+    _check_output(wl, out, torch.arange(wl.T))
+
+
+@pytest.mark.parametrize("name", ["c2_t1024_o0", "c2_t1024_o64", "c2_t1024_o128", "c2_t1024_o224"])
+def test_output_parity_mid(name):
+    log(f"test_output_parity_mid[{name}]")
+    wl = W.standard(name)
+    out = run_gpu(wl, fill=float("nan"))
+    _check_output(wl, out, spread_tokens(wl.T, 256))
+
+
+@pytest.mark.parametrize("name", ["c3_t8192", "c4_t14000_skew"])
+def test_output_parity_large(name):
+    log(f"test_output_parity_large[{name}]")
+    wl = W.standard(name)
+    out = run_gpu(wl, fill=float("nan"))
+    assert torch.isfinite(out.float()).all()
+    _check_output(wl, out, spread_tokens(wl.T, 48))
+
+
+def test_sort_stage_bit_exact():
+    """Expert offsets, slot order (token-ascending per expert) and per-token
+    slot lists from the workspace equal the oracle's local assignment."""
+    from flashinfer_amd import _lib, kernel
+    from oracle import ref_moe as R
+    log("test_sort_stage_bit_exact")
+    wl = W.standard("c2_t1024_o64")
+    run_gpu(wl)
+    L = _lib.workspace_layout(wl.T)
+    ws = kernel.last_workspace().cpu()
+    T = wl.T
+    eoff = ws[L.expert_off:L.expert_off + 33 * 4].view(torch.int32)
+    r = R.route(wl.tensors["routing_logits"], wl.tensors["routing_bias"], wl.routed_scaling_factor)
+    slots = R.local_assignment(r.ids, r.weights, wl.local_expert_offset, 32)
+    counts = torch.tensor([len(tk) for tk, _ in slots])
+    want_off = torch.cat([torch.zeros(1, dtype=torch.long), counts.cumsum(0)])
+    assert torch.equal(eoff.long(), want_off)
+    S = int(want_off[-1])
+    stok = ws[L.sorted_tok:L.sorted_tok + S * 4].view(torch.int32).long()
+    sw = ws[L.sorted_w:L.sorted_w + S * 4].view(torch.float32)
+    assert torch.equal(stok, torch.cat([tk for tk, _ in slots]))
+    assert torch.allclose(sw, torch.cat([w for _, w in slots]), rtol=1e-6, atol=0)
+    tslot = ws[L.tok_slot:L.tok_slot + T * 8 * 4].view(torch.int32).view(T, 8).long()
+    for t in range(0, T, 7):
+        mine = [int(s) for s in tslot[t] if s >= 0]
+        assert all(int(stok[s]) == t for s in mine)
+        exp = [int(want_off[e]) + int((slots[e][0] == t).nonzero()[0]) for e in range(32)
+               if bool((slots[e][0] == t).any())]
+        assert mine == exp
+        assert all(int(s) == -1 for s in tslot[t][len(mine):])
+
+
+def test_gemm1_stage_against_oracle():
+    """SwiGLU(GEMM1) rows in the workspace against the oracle's fp32 values."""
+    from flashinfer_amd import _lib, kernel
+    from oracle import ref_moe as R
+    log("test_gemm1_stage_against_oracle")
+    wl = W.standard("c1_t64")
+    run_gpu(wl)
+    L = _lib.workspace_layout(wl.T)
+    ws = kernel.last_workspace()
+    t = wl.tensors
+    r = R.route(t["routing_logits"], t["routing_bias"], wl.routed_scaling_factor)
+    slots = R.local_assignment(r.ids, r.weights, wl.local_expert_offset, 32)
+    a = R.dequant_activations(t["hidden_states"], t["hidden_states_scale"])
+    S = sum(len(tk) for tk, _ in slots)
+    act = ws[L.act:L.act + S * 2048 * 2].view(torch.bfloat16).view(S, 2048).float().cpu()
+    row = 0
+    worst = 0.0
+    for e, (tk, _) in enumerate(slots):
+        if len(tk) == 0:
+            continue
+        g = a[tk] @ R.dequant_blocks(t["gemm1_weights"][e], t["gemm1_weights_scale"][e]).t()
+        x = R.swiglu(g)
+        got = act[row:row + len(tk)]
+        rep = R.tolerance_report(got, x)
+        worst = max(worst, rep["normwise_rel"])
+        assert rep["n_bad"] == 0, (e, rep)
+        row += len(tk)
+    log(f"gemm1 stage worst normwise rel {worst:.2e}")
+
+
+def test_deterministic_bitwise():
+    log("test_deterministic_bitwise")
+    wl = W.standard("c2_t1024_o0")
+    a = run_gpu(wl)
+    b = run_gpu(wl, fill=1.0)
+    assert torch.equal(a.view(torch.int16), b.view(torch.int16))
+
+
+def test_empty_routing_zero_fill():
+    log("test_empty_routing_zero_fill")
+    wl = W.standard("c1_t64", local_expert_offset=256)
+    out = run_gpu(wl, fill=float("nan"))
+    assert torch.count_nonzero(out.float().nan_to_num(1.0)) == 0
+
+
+def test_skew_all_rows_on_biased_experts():
+    """Full-size property at T=14000: every token routes to exactly the 8
+    biased local experts, so S = 8T and experts 8..31 are empty."""
+    from flashinfer_amd import _lib, kernel
+    log("test_skew_all_rows_on_biased_experts")
+    wl = W.standard("c4_t14000_skew")
+    run_gpu(wl)
+    L = _lib.workspace_layout(wl.T)
+    eoff = kernel.last_workspace()[L.expert_off:L.expert_off + 33 * 4].view(torch.int32).cpu()
+    want = torch.tensor([min(e, 8) * wl.T for e in range(33)], dtype=torch.int32)
+    assert torch.equal(eoff, want)
+
+
+def test_scalar_tensor_arguments():
+    """Scalars given as 0-d tensors behave like Python numbers (kernel.py:547-548)."""
+    from flashinfer_amd import kernel
+    log("test_scalar_tensor_arguments")
+    wl = W.standard("c1_t16")
+    a = run_gpu(wl)
+    args = gpu_args(wl)
+    args[8] = torch.tensor(wl.local_expert_offset)
+    args[9] = torch.tensor(wl.routed_scaling_factor)
+    out = torch.empty_like(a)
+    kernel.run(*args, out)
+    torch.cuda.synchronize()
+    assert torch.equal(a.view(torch.int16), out.view(torch.int16))
