@@ -1,0 +1,238 @@
+"""Benchmark of the fused MoE on one MI355X.
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload c1_t64]
+                    [--sweep | --no-sweep] [--no-cpu]
+
+A step is one call of ``flashinfer_amd.kernel.run`` on the workload's
+synthetic inputs, already resident in HBM. The headline workload is the
+decode sweep's T=64 point (H=7168, I=2048, 32 local experts of 256, top-8,
+FP8 e4m3 block-scaled), which streams the active experts' weights and is
+bound by HBM bandwidth. W untimed calls, then 5 trials of K calls each,
+bracketed by ``torch.cuda.synchronize()``; ``value`` is the median trial's
+microseconds per call. Every call records HIP events between its five
+kernels on the stream they run on, which gives each kernel's average
+duration over the timed region.
+
+Rank 0 prints ONE JSON line. ``roofline`` covers the dominant kernel
+(GEMM1+SwiGLU at decode); ``call_roofline`` the whole call; ``sweep`` the
+other configurations; ``cpu_baseline`` the CPU oracle on this host.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import statistics
+import sys
+import time
+
+import torch
+
+HBM_PEAK_GBS = 8000.0        # MI355X HBM3E, GB/s
+FP8_PEAK_TFLOPS = 5000.0     # dense FP8 MFMA, TFLOP/s
+BF16_PEAK_TFLOPS = 2500.0    # dense BF16 MFMA, TFLOP/s
+H, I, E_GLOBAL, BLOCK = 7168, 2048, 256, 128
+
+# Algorithmic bytes: weights + block scales of each active expert, plus the
+# per-token and per-slot rows a kernel must read or write once.
+W1_EXPERT_BYTES = 2 * I * H + (2 * I // BLOCK) * (H // BLOCK) * 4        # 29,367,296
+W2_EXPERT_BYTES = H * I + (H // BLOCK) * (I // BLOCK) * 4                # 14,683,648
+HS_ROW_BYTES = H + (H // BLOCK) * 4                                      # fp8 row + scales
+ACT_ROW_BYTES = I * 2                                                    # bf16 SwiGLU row
+PART_ROW_BYTES = H * 4                                                   # fp32 GEMM2 row
+GEMM1_FLOPS_PER_SLOT = 2 * 2 * I * H
+GEMM2_FLOPS_PER_SLOT = 2 * H * I
+
+SWEEP = ["c1_t1", "c1_t4", "c1_t16", "c1_t64", "t256", "c2_t1024_o0", "c3_t8192",
+         "c4_t14000_skew"]
+
+
+def log(msg):
+    print(msg, file=sys.stderr, flush=True)
+
+
+def call_bytes(T, A_e):
+    return T * (E_GLOBAL * 4 + HS_ROW_BYTES + H * 2) + E_GLOBAL * 2 + A_e * (W1_EXPERT_BYTES + W2_EXPERT_BYTES)
+
+
+def gemm1_bytes(S, A_e):
+    return A_e * W1_EXPERT_BYTES + S * (HS_ROW_BYTES + ACT_ROW_BYTES)
+
+
+def gemm2_bytes(S, A_e):
+    return A_e * W2_EXPERT_BYTES + S * (ACT_ROW_BYTES + PART_ROW_BYTES)
+
+
+def make(name):
+    from flashinfer_amd import workloads as W
+    if name == "t256":
+        return W.make_workload("t256", T=256, seed=111, local_expert_offset=0)
+    return W.standard(name)
+
+
+def routing_stats(T):
+    from flashinfer_amd import _lib, kernel
+    L = _lib.workspace_layout(T)
+    eoff = kernel.last_workspace()[L.expert_off:L.expert_off + 33 * 4].view(torch.int32).cpu()
+    counts = (eoff[1:] - eoff[:-1]).tolist()
+    return int(eoff[-1]), sum(1 for c in counts if c > 0), max(counts) if counts else 0
+
+
+_DEV_W = {}
+
+
+def device_args(wl, dev):
+    """Per-token tensors copied to the GPU; the shared weights are copied once."""
+    names = ["gemm1_weights", "gemm1_weights_scale", "gemm2_weights", "gemm2_weights_scale"]
+    if not _DEV_W:
+        for n in names:
+            _DEV_W[n] = wl.tensors[n].to(dev)
+    t = wl.tensors
+    return [t["routing_logits"].to(dev), t["routing_bias"].to(dev), t["hidden_states"].to(dev),
+            t["hidden_states_scale"].to(dev)] + [_DEV_W[n] for n in names] + [
+        wl.local_expert_offset, wl.routed_scaling_factor]
+
+
+def time_workload(wl, steps, warmup, trials=5):
+    from flashinfer_amd import _lib, kernel
+    dev = torch.device("cuda", 0)
+    args = device_args(wl, dev)
+    out = torch.empty(wl.T, H, dtype=torch.bfloat16, device=dev)
+    for _ in range(warmup):
+        kernel.run(*args, out)
+    torch.cuda.synchronize()
+    S, A_e, max_rows = routing_stats(wl.T)
+    nev = _lib.NUM_PHASES + 1
+    ev = [[torch.cuda.Event(enable_timing=True) for _ in range(nev)] for _ in range(steps)]
+    trial_us = []
+    phase_sum = [0.0] * _lib.NUM_PHASES
+    for tr in range(trials):
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for k in range(steps):
+            kernel.run_profiled(*args, out, events=ev[k])
+        torch.cuda.synchronize()
+        trial_us.append((time.perf_counter() - t0) * 1e6 / steps)
+        for k in range(steps):
+            for p in range(_lib.NUM_PHASES):
+                phase_sum[p] += ev[k][p].elapsed_time(ev[k][p + 1]) * 1e3
+    phase_us = [s / (steps * trials) for s in phase_sum]
+    us = statistics.median(trial_us)
+    B = call_bytes(wl.T, A_e)
+    F1, F2 = S * GEMM1_FLOPS_PER_SLOT, S * GEMM2_FLOPS_PER_SLOT
+    F = F1 + F2
+    t = us * 1e-6
+    bound_t = max(B / (HBM_PEAK_GBS * 1e9), F / (FP8_PEAK_TFLOPS * 1e12))
+    res = {
+        "workload": wl.name, "T": wl.T, "local_expert_offset": wl.local_expert_offset,
+        "slots": S, "active_experts": A_e, "max_rows_per_expert": max_rows,
+        "us_per_call": round(us, 2), "trials_us": [round(x, 2) for x in trial_us],
+        "gbps": round(B / t / 1e9, 1), "tflops": round(F / t / 1e12, 2),
+        "hbm_frac": round(B / t / 1e9 / HBM_PEAK_GBS, 4),
+        "fp8_frac": round(F / t / 1e12 / FP8_PEAK_TFLOPS, 4),
+        "roofline_frac": round(bound_t / t, 4),
+        "algorithmic_bytes": B, "algorithmic_flops": F,
+        "phase_us": {n: round(v, 2) for n, v in zip(_lib.PHASES, phase_us)},
+    }
+    g1 = phase_us[2] * 1e-6
+    g2 = phase_us[3] * 1e-6
+    res["gemm1_gbps"] = round(gemm1_bytes(S, A_e) / g1 / 1e9, 1) if g1 > 0 else None
+    res["gemm1_tflops"] = round(F1 / g1 / 1e12, 2) if g1 > 0 else None
+    res["gemm2_gbps"] = round(gemm2_bytes(S, A_e) / g2 / 1e9, 1) if g2 > 0 else None
+    res["gemm2_tflops"] = round(F2 / g2 / 1e12, 2) if g2 > 0 else None
+    del args, out
+    return res
+
+
+def cpu_baseline(wl, reps=3):
+    """The CPU oracle (fp32 torch) on this host: 1 warmup + reps timed calls."""
+    from oracle import ref_moe as R
+    torch.set_num_threads(os.cpu_count() or 1)
+    cores = torch.get_num_threads()
+    args = wl.args()
+    R.moe_forward(*args)
+    ts = []
+    for _ in range(reps):
+        t0 = time.perf_counter()
+        R.moe_forward(*args)
+        ts.append(time.perf_counter() - t0)
+    return {"value": round(statistics.median(ts) * 1e6, 1), "unit": "us/call", "cores": cores,
+            "kind": "port",
+            "sample": f"full {wl.name} call (T={wl.T}), fp32 torch oracle, dequantising only the "
+                      f"active experts, 1 warmup + {reps} timed, median"}
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=100)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--workload", default="c1_t64")
+    ap.add_argument("--sweep", dest="sweep", action="store_true", default=True)
+    ap.add_argument("--no-sweep", dest="sweep", action="store_false")
+    ap.add_argument("--no-cpu", action="store_true")
+    a = ap.parse_args()
+    if a.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print("bench.py measures one GPU: this operator is one expert-parallel shard "
+              "(local_expert_offset selects the shard) and has no multi-GPU path. "
+              "Run with --gpus 1.", file=sys.stderr)
+        sys.exit(2)
+    if not torch.cuda.is_available():
+        print("bench.py needs a ROCm GPU", file=sys.stderr)
+        sys.exit(2)
+    from flashinfer_amd import _lib
+    _lib.lib()
+
+    t_start = time.time()
+    wl = make(a.workload)
+    log(f"[bench] inputs for {a.workload} ready in {time.time() - t_start:.1f}s")
+    head = time_workload(wl, a.steps, a.warmup)
+    log(f"[bench] {json.dumps(head)}")
+
+    sweep = []
+    if a.sweep:
+        for name in SWEEP:
+            if name == a.workload:
+                sweep.append(head)
+                continue
+            w = make(name)
+            steps = a.steps if w.T <= 1024 else max(10, a.steps // 5)
+            r = time_workload(w, steps, a.warmup)
+            log(f"[bench] {json.dumps(r)}")
+            sweep.append(r)
+            del w
+    cpu = None
+    if not a.no_cpu:
+        log("[bench] CPU oracle baseline ...")
+        cpu = cpu_baseline(wl)
+        log(f"[bench] cpu {cpu}")
+
+    g1_us = head["phase_us"]["gemm1_swiglu"]
+    g1_bytes = gemm1_bytes(head["slots"], head["active_experts"])
+    achieved = g1_bytes / (g1_us * 1e-6) / 1e9 if g1_us > 0 else 0.0
+    line = {
+        "metric": "fused-MoE µs/call + FP8 TFLOP/s & HBM GB/s vs roofline at T=1/256/8192",
+        "value": head["us_per_call"], "unit": "us/call", "n_gpus": 1, "steps": a.steps,
+        "warmup": a.warmup, "ms_per_step": round(head["us_per_call"] / 1000.0, 5),
+        "higher_is_better": False, "scaling": "weak", "vs_baseline": None, "dtype": "fp8_e4m3 (GEMM1) / bf16 (GEMM2), fp32 accumulate",
+        "data": "synthetic (seeded N(0,1) fp8 weights/activations, U scales, N(0,0.1) bias)",
+        "config": {"workload": f"decode sweep T={wl.T} (configs[1])", "T": wl.T,
+                   "H": H, "I": I, "experts_global": E_GLOBAL, "experts_local": 32, "top_k": 8,
+                   "local_expert_offset": wl.local_expert_offset,
+                   "slots": head["slots"], "active_experts": head["active_experts"],
+                   "parallelism": "single GPU (one EP shard)"},
+        "roofline": {"kernel": "gemm1_swiglu", "bound": "hbm", "achieved": round(achieved, 1),
+                     "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
+                     "algorithmic_bytes_per_launch": g1_bytes, "avg_launch_us": round(g1_us, 2)},
+        "call_roofline": {"gbps": head["gbps"], "hbm_frac": head["hbm_frac"],
+                          "tflops": head["tflops"], "roofline_frac": head["roofline_frac"],
+                          "phase_us": head["phase_us"]},
+        "cpu_baseline": cpu,
+        "sweep": sweep,
+    }
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()
