@@ -16,7 +16,8 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 CSRC = os.path.join(HERE, "csrc")
 BUILD = os.path.join(HERE, "_build")
 LIB = os.path.join(HERE, "libmi_moe.so")
-SOURCES = ["route.hip", "sort.hip", "gemm1.hip", "gemm2.hip", "combine.hip", "capi.hip"]
+SOURCES = ["route.hip", "sort.hip", "gemm1.hip", "gemm2.hip", "gemm1_tile.hip", "gemm2_tile.hip",
+           "combine.hip", "capi.hip"]
 ARCH = "gfx950"
 
 HIPCC_FLAGS = [

@@ -9,6 +9,7 @@
 #include <math.h>
 #include <stdarg.h>
 #include <stdio.h>
+#include <stdlib.h>
 
 #include <string>
 
@@ -55,11 +56,27 @@ mi_moe_layout make_layout(int64_t T) {
 
 bool aligned(const void* p, size_t a) { return ((uintptr_t)p % a) == 0; }
 
-// Kernel variants by token count (weights stream once per row tile).
-int pick_variant(int64_t T) {
-    if (T <= 128) return 0;
-    if (T <= 1024) return 1;
-    return 2;
+// GEMM variants by token count. MI_MOE_VARIANT="v" or "v1,v2" overrides
+// (0..NUM_VARIANTS-1, for tests and tuning).
+struct Variants {
+    int g1, g2;
+};
+
+Variants pick_variants(int64_t T) {
+    Variants v;
+    if (T <= 128) v = {0, 0};
+    else if (T <= 1024) v = {1, 1};
+    else if (T <= 2048) v = {4, 4};
+    else v = {3, 3};
+    const char* env = getenv("MI_MOE_VARIANT");
+    if (env && *env) {
+        int a = -1, b = -1;
+        const int n = sscanf(env, "%d,%d", &a, &b);
+        if (n >= 1 && a >= 0 && a < NUM_VARIANTS) v.g1 = a;
+        if (n == 2 && b >= 0 && b < NUM_VARIANTS) v.g2 = b;
+        else if (n == 1 && a >= 0 && a < NUM_VARIANTS) v.g2 = a;
+    }
+    return v;
 }
 
 }  // namespace
@@ -168,7 +185,7 @@ static int run_impl(const mi_moe_args* a, hipStream_t s, hipEvent_t const* ev) {
     p.act = (uint16_t*)(ws + L.act);
     p.part = (float*)(ws + L.part);
 
-    const int variant = pick_variant(T);
+    const Variants var = pick_variants(T);
     hipError_t err = hipSuccess;
     auto mark = [&](int i) {
         if (ev && err == hipSuccess) err = hipEventRecord(ev[i], s);
@@ -178,13 +195,13 @@ static int run_impl(const mi_moe_args* a, hipStream_t s, hipEvent_t const* ev) {
         err = launch_route(a->routing_logits, a->routing_bias, a->bias_dtype == MI_MOE_DTYPE_F32,
                            p.T, p.rsf, p.topk_ids, p.topk_w, s);
     mark(1);
-    if (err == hipSuccess) err = launch_sort(p, gemm1_bm(variant), gemm2_bm(variant), s);
+    if (err == hipSuccess) err = launch_sort(p, gemm1_bm(var.g1), gemm2_bm(var.g2), s);
     mark(2);
     if (err == hipSuccess)
         err = launch_gemm1(p, a->hidden_states, a->hidden_states_scale, a->gemm1_weights,
-                           a->gemm1_weights_scale, variant, s);
+                           a->gemm1_weights_scale, var.g1, s);
     mark(3);
-    if (err == hipSuccess) err = launch_gemm2(p, a->gemm2_weights, a->gemm2_weights_scale, variant, s);
+    if (err == hipSuccess) err = launch_gemm2(p, a->gemm2_weights, a->gemm2_weights_scale, var.g2, s);
     mark(4);
     if (err == hipSuccess) err = launch_combine(p, (uint16_t*)a->output, s);
     mark(5);

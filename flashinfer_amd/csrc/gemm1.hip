@@ -119,11 +119,20 @@ __global__ __launch_bounds__(256) void gemm1_stream_kernel(Plan p, const uint8_t
     }
 }
 
-int gemm1_bm(int variant) { return variant == 0 ? 16 : (variant == 1 ? 32 : 64); }
+int gemm1_bm(int variant) {
+    switch (variant) {
+        case 0: return 16;
+        case 1: return 32;
+        case 2: return 64;
+        case 3: return 256;
+        default: return 128;
+    }
+}
 
 hipError_t launch_gemm1(const Plan& p, const uint8_t* hs, const float* hs_scale, const uint8_t* w1,
                         const float* w1s, int variant, hipStream_t s) {
     if (p.T <= 0) return hipSuccess;
+    if (variant >= 3) return launch_gemm1_tile(p, hs, hs_scale, w1, w1s, variant, s);
     const int bm = gemm1_bm(variant);
     dim3 grid(I / 64, max_mtiles(p.T, bm));
     switch (variant) {

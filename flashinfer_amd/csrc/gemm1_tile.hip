@@ -1,0 +1,190 @@
+// Grouped FP8 GEMM1 + SwiGLU, LDS-tiled variant for many rows per expert.
+//
+// Same contract as gemm1_stream_kernel (solution/triton/kernel.py:69-186 and
+// :301-330): act[s, j] = silu(G[s, I+j]) * G[s, j] with
+//   G[s, n] = sum_kb sa[kb, tok(s)] * sb1[e, n/128, kb] * (A8[tok(s), kb-block] . W1[e, n, kb-block]).
+//
+// A workgroup of WM x WN waves computes a tile of BM = 64*WM rows (slots of
+// one expert) by BG = 64*WN gate columns plus the BG matching up columns.
+// Per 128-wide k-block (one scale block) the A rows (gathered by token), the
+// 2*BG weight rows and the BM activation scales are copied global -> LDS
+// with global_load_lds_dwordx4 into one of two stages, so the copy of
+// k-block kb+1 overlaps the MFMAs on kb; one barrier per k-block.
+// Each wave owns 64 rows x (64 gate + 64 up) columns: 4 x 8 MFMA tiles of
+// v_mfma_scale_f32_16x16x128_f8f6f4, each scaled by sa*sb in fp32 as it is
+// accumulated. The SwiGLU epilogue pairs gate and up columns in registers.
+//
+// LDS rows are 128 bytes; 16-byte chunk c of row r sits at position
+// c ^ swz8(r), so the 16 rows read by lanes 0..15 hit distinct banks.
+#include "tile_common.hpp"
+
+namespace mimoe {
+
+template <int WM, int WN>
+struct G1Tile {
+    static constexpr int NW = WM * WN;
+    static constexpr int THREADS = 64 * NW;
+    static constexpr int BM = 64 * WM;
+    static constexpr int BG = 64 * WN;
+    static constexpr int NT = I / BG;
+    static constexpr int A_BYTES = BM * BLK;
+    static constexpr int B_BYTES = 2 * BG * BLK;
+    static constexpr int SA_BYTES = BM * 4;
+    static constexpr int STAGE = A_BYTES + B_BYTES + SA_BYTES;
+    static constexpr int A_LD = A_BYTES / 1024 / NW;  // 1 KB copies per wave per stage
+    static constexpr int B_LD = B_BYTES / 1024 / NW;
+    static constexpr int SA_WAVES = BM / 64;          // waves copying one scale each per lane
+    static_assert(A_BYTES % (1024 * NW) == 0 && B_BYTES % (1024 * NW) == 0, "loader split");
+    static_assert(SA_WAVES <= NW, "scale loader");
+    static_assert(2 * STAGE <= 160 * 1024, "LDS budget");
+};
+
+template <int WM, int WN, int GM>
+__global__ __launch_bounds__(64 * WM * WN) void gemm1_tile_kernel(
+    Plan p, const uint8_t* __restrict__ hs, const float* __restrict__ hs_scale,
+    const uint8_t* __restrict__ w1, const float* __restrict__ w1s) {
+    using C = G1Tile<WM, WN>;
+    __shared__ __attribute__((aligned(1024))) uint8_t smem[2 * C::STAGE];
+
+    int e, row0, nrows, nt;
+    if (!tile_coords<C::NT, GM>(p.meta, META_MTILE1, C::BM, e, row0, nrows, nt)) return;
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int jb = nt * C::BG;
+
+    // Loader: in its i-th copy, wave w fills LDS rows 8*(w*LD + i) .. +7;
+    // lane l takes row +l/8, chunk position l%8.
+    uint32_t a_off[C::A_LD], b_off[C::B_LD];
+#pragma unroll
+    for (int i = 0; i < C::A_LD; ++i) {
+        const int row = 8 * (wave * C::A_LD + i) + (lane >> 3);
+        const int c = (lane & 7) ^ swz8(row);
+        const int tok = p.sorted_tok[row0 + min(row, nrows - 1)];
+        a_off[i] = (uint32_t)tok * H + c * 16;
+    }
+#pragma unroll
+    for (int i = 0; i < C::B_LD; ++i) {
+        const int row = 8 * (wave * C::B_LD + i) + (lane >> 3);
+        const int c = (lane & 7) ^ swz8(row);
+        const int wrow = row < C::BG ? jb + row : I + jb + (row - C::BG);
+        b_off[i] = (uint32_t)((e * N1 + wrow) * H + c * 16);
+    }
+    uint32_t sa_off = 0;
+    if (wave < C::SA_WAVES) {
+        const int row = 64 * wave + lane;
+        sa_off = (uint32_t)p.sorted_tok[row0 + min(row, nrows - 1)];
+    }
+
+    auto issue = [&](int stage, int kb) __attribute__((always_inline)) {
+        uint8_t* s = smem + stage * C::STAGE;
+#pragma unroll
+        for (int i = 0; i < C::A_LD; ++i)
+            g2l16(hs + a_off[i] + kb * BLK, s + (wave * C::A_LD + i) * 1024);
+#pragma unroll
+        for (int i = 0; i < C::B_LD; ++i)
+            g2l16(w1 + b_off[i] + kb * BLK, s + C::A_BYTES + (wave * C::B_LD + i) * 1024);
+        if (wave < C::SA_WAVES)
+            g2l4(hs_scale + (size_t)kb * p.T + sa_off, s + C::A_BYTES + C::B_BYTES + wave * 256);
+    };
+
+    const int wm = wave % WM, wn = wave / WM;
+    const int r = lane & 15, g = lane >> 4;
+    const float* sbg_p = w1s + ((size_t)e * N1B + jb / BLK) * HB;
+    const float* sbu_p = w1s + ((size_t)e * N1B + (I + jb) / BLK) * HB;
+
+    v4f acc[4][8];
+    const v4f zero = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int m = 0; m < 4; ++m)
+#pragma unroll
+        for (int n = 0; n < 8; ++n) acc[m][n] = zero;
+
+    issue(0, 0);
+    wait_vmem();
+    __syncthreads();
+
+#pragma unroll 1
+    for (int kb = 0; kb < HB; ++kb) {
+        const int cur = kb & 1;
+        if (kb + 1 < HB) issue(cur ^ 1, kb + 1);
+        const uint8_t* sA = smem + cur * C::STAGE;
+        const uint8_t* sB = sA + C::A_BYTES;
+        const float* sSA = reinterpret_cast<const float*>(sB + C::B_BYTES);
+
+        v8i a[4];
+        float cg[4][4], cu[4][4];
+        const float sg = sbg_p[kb];
+        const float su = sbu_p[kb];
+#pragma unroll
+        for (int m = 0; m < 4; ++m) {
+            const int row = wm * 64 + m * 16 + r;
+            const uint8_t* base = sA + row * BLK;
+            const int sw = swz8(row);
+            const v4i lo = lds16(base + ((g ^ sw) << 4));
+            const v4i hi = lds16(base + (((g + 4) ^ sw) << 4));
+            a[m] = (v8i){lo.x, lo.y, lo.z, lo.w, hi.x, hi.y, hi.z, hi.w};
+            const float4 s4 = *reinterpret_cast<const float4*>(sSA + wm * 64 + m * 16 + g * 4);
+            cg[m][0] = s4.x * sg; cg[m][1] = s4.y * sg; cg[m][2] = s4.z * sg; cg[m][3] = s4.w * sg;
+            cu[m][0] = s4.x * su; cu[m][1] = s4.y * su; cu[m][2] = s4.z * su; cu[m][3] = s4.w * su;
+        }
+#pragma unroll
+        for (int n = 0; n < 8; ++n) {
+            const int brow = (n < 4) ? (wn * 64 + n * 16 + r) : (C::BG + wn * 64 + (n - 4) * 16 + r);
+            const uint8_t* base = sB + brow * BLK;
+            const int sw = swz8(brow);
+            const v4i lo = lds16(base + ((g ^ sw) << 4));
+            const v4i hi = lds16(base + (((g + 4) ^ sw) << 4));
+            const v8i b = (v8i){lo.x, lo.y, lo.z, lo.w, hi.x, hi.y, hi.z, hi.w};
+#pragma unroll
+            for (int m = 0; m < 4; ++m) {
+                const v4f pr = mfma_f8_16x16x128(a[m], b, zero);
+                const float* sc = (n < 4) ? cg[m] : cu[m];
+                acc[m][n][0] += pr[0] * sc[0];
+                acc[m][n][1] += pr[1] * sc[1];
+                acc[m][n][2] += pr[2] * sc[2];
+                acc[m][n][3] += pr[3] * sc[3];
+            }
+        }
+        wait_vmem();
+        __syncthreads();
+    }
+
+#pragma unroll
+    for (int m = 0; m < 4; ++m) {
+#pragma unroll
+        for (int n = 0; n < 4; ++n) {
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const int row = wm * 64 + m * 16 + g * 4 + i;
+                if (row < nrows) {
+                    const float v = silu(acc[m][n + 4][i]) * acc[m][n][i];
+                    p.act[(size_t)(row0 + row) * I + jb + wn * 64 + n * 16 + r] = f2bf(v);
+                }
+            }
+        }
+    }
+}
+
+int gemm1_tile_bm(int variant) { return variant == 3 ? 256 : 128; }
+
+hipError_t launch_gemm1_tile(const Plan& p, const uint8_t* hs, const float* hs_scale,
+                             const uint8_t* w1, const float* w1s, int variant, hipStream_t s) {
+    if (variant == 3) {
+        using C = G1Tile<4, 2>;
+        const int tiles = max_mtiles(p.T, C::BM) * C::NT;
+        dim3 grid((tiles + 7) / 8 * 8);
+        hipLaunchKernelGGL((gemm1_tile_kernel<4, 2, 4>), grid, dim3(C::THREADS), 0, s, p, hs,
+                           hs_scale, w1, w1s);
+    } else {
+        using C = G1Tile<2, 2>;
+        const int tiles = max_mtiles(p.T, C::BM) * C::NT;
+        dim3 grid((tiles + 7) / 8 * 8);
+        hipLaunchKernelGGL((gemm1_tile_kernel<2, 2, 4>), grid, dim3(C::THREADS), 0, s, p, hs,
+                           hs_scale, w1, w1s);
+    }
+    return hipGetLastError();
+}
+
+}  // namespace mimoe

@@ -129,11 +129,20 @@ __global__ __launch_bounds__(256) void gemm2_stream_kernel(Plan p, const uint8_t
     }
 }
 
-int gemm2_bm(int variant) { return variant == 0 ? 16 : (variant == 1 ? 32 : 64); }
+int gemm2_bm(int variant) {
+    switch (variant) {
+        case 0: return 16;
+        case 1: return 32;
+        case 2: return 64;
+        case 3: return 128;
+        default: return 64;
+    }
+}
 
 hipError_t launch_gemm2(const Plan& p, const uint8_t* w2, const float* w2s, int variant,
                         hipStream_t s) {
     if (p.T <= 0) return hipSuccess;
+    if (variant >= 3) return launch_gemm2_tile(p, w2, w2s, variant, s);
     const int bm = gemm2_bm(variant);
     dim3 grid(HB, max_mtiles(p.T, bm));
     switch (variant) {

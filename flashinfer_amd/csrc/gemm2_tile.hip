@@ -1,0 +1,176 @@
+// Grouped GEMM2 (down projection), LDS-tiled variant for many rows per expert.
+//
+// Same contract as gemm2_stream_kernel (solution/triton/kernel.py:193-293):
+//   part[s, n] = sum_kb sb2[e, n/128, kb] * (act[s, kb-block] . W2[e, n, kb-block])
+// with bf16 activations and fp8 weights widened to bf16 (exact).
+//
+// A workgroup of WM x WN waves computes BM = 64*WM rows x BN = 64*WN output
+// columns. Per 128-wide k-block the BM activation rows (256 B each, bf16) and
+// the BN fp8 weight rows (128 B each) are copied global -> LDS with
+// global_load_lds_dwordx4 into one of two stages (copy of kb+1 overlaps the
+// MFMAs on kb). Each wave owns 64 x 64 outputs: for each 16-column weight
+// fragment it converts 32 fp8 -> bf16 once and feeds four 16-row fragments,
+// four v_mfma_f32_16x16x32_bf16 per 128-k block, then scales the block's
+// partial sum by sb2 in fp32.
+//
+// Operand k order (identical for A and B, so the pairing is exact): lane
+// (r = l%16, g = l/16) holds k-block offsets 16g+[0,16) and 64+16g+[0,16);
+// MFMA h uses offsets 16g+8h (h<2) and 64+16g+8(h-2) (h>=2).
+// LDS: weight rows are 128 B with swz8; activation rows are 256 B (16
+// chunks) with chunk c at position c ^ (row & 15).
+#include "tile_common.hpp"
+
+namespace mimoe {
+
+template <int WM, int WN>
+struct G2Tile {
+    static constexpr int NW = WM * WN;
+    static constexpr int THREADS = 64 * NW;
+    static constexpr int BM = 64 * WM;
+    static constexpr int BN = 64 * WN;
+    static constexpr int NT = H / BN;
+    static constexpr int A_BYTES = BM * BLK * 2;
+    static constexpr int B_BYTES = BN * BLK;
+    static constexpr int STAGE = A_BYTES + B_BYTES;
+    static constexpr int A_LD = A_BYTES / 1024 / NW;
+    static constexpr int B_LD = B_BYTES / 1024 / NW;
+    static_assert(H % BN == 0, "n tiles");
+    static_assert(A_BYTES % (1024 * NW) == 0 && B_BYTES % (1024 * NW) == 0, "loader split");
+    static_assert(2 * STAGE <= 160 * 1024, "LDS budget");
+};
+
+template <int WM, int WN, int GM>
+__global__ __launch_bounds__(64 * WM * WN) void gemm2_tile_kernel(Plan p,
+                                                                  const uint8_t* __restrict__ w2,
+                                                                  const float* __restrict__ w2s) {
+    using C = G2Tile<WM, WN>;
+    __shared__ __attribute__((aligned(1024))) uint8_t smem[2 * C::STAGE];
+
+    int e, row0, nrows, nt;
+    if (!tile_coords<C::NT, GM>(p.meta, META_MTILE2, C::BM, e, row0, nrows, nt)) return;
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int n0 = nt * C::BN;
+
+    // Activation loader: a 1 KB copy covers 4 rows of 256 B; lane l takes
+    // row +l/16, chunk position l%16.
+    const uint8_t* act = reinterpret_cast<const uint8_t*>(p.act);
+    uint32_t a_off[C::A_LD], b_off[C::B_LD];
+#pragma unroll
+    for (int i = 0; i < C::A_LD; ++i) {
+        const int row = 4 * (wave * C::A_LD + i) + (lane >> 4);
+        const int c = (lane & 15) ^ swz16(row);
+        a_off[i] = (uint32_t)(row0 + min(row, nrows - 1)) * (I * 2) + c * 16;
+    }
+#pragma unroll
+    for (int i = 0; i < C::B_LD; ++i) {
+        const int row = 8 * (wave * C::B_LD + i) + (lane >> 3);
+        const int c = (lane & 7) ^ swz8(row);
+        b_off[i] = (uint32_t)((e * H + n0 + row) * I + c * 16);
+    }
+
+    auto issue = [&](int stage, int kb) __attribute__((always_inline)) {
+        uint8_t* s = smem + stage * C::STAGE;
+#pragma unroll
+        for (int i = 0; i < C::A_LD; ++i)
+            g2l16(act + (size_t)a_off[i] + kb * (BLK * 2), s + (wave * C::A_LD + i) * 1024);
+#pragma unroll
+        for (int i = 0; i < C::B_LD; ++i)
+            g2l16(w2 + b_off[i] + kb * BLK, s + C::A_BYTES + (wave * C::B_LD + i) * 1024);
+    };
+
+    const int wm = wave % WM, wn = wave / WM;
+    const int r = lane & 15, g = lane >> 4;
+    const float* sb_p = w2s + ((size_t)e * HB + (n0 + wn * 64) / BLK) * IB;
+
+    v4f acc[4][4];
+    const v4f zero = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int m = 0; m < 4; ++m)
+#pragma unroll
+        for (int n = 0; n < 4; ++n) acc[m][n] = zero;
+
+    issue(0, 0);
+    wait_vmem();
+    __syncthreads();
+
+#pragma unroll 1
+    for (int kb = 0; kb < IB; ++kb) {
+        const int cur = kb & 1;
+        if (kb + 1 < IB) issue(cur ^ 1, kb + 1);
+        const uint8_t* sA = smem + cur * C::STAGE;
+        const uint8_t* sB = sA + C::A_BYTES;
+        const float sb = sb_p[kb];
+
+        v4i a[4][4];
+#pragma unroll
+        for (int m = 0; m < 4; ++m) {
+            const int row = wm * 64 + m * 16 + r;
+            const uint8_t* base = sA + row * (BLK * 2);
+            const int sw = swz16(row);
+            a[m][0] = lds16(base + (((2 * g) ^ sw) << 4));
+            a[m][1] = lds16(base + (((2 * g + 1) ^ sw) << 4));
+            a[m][2] = lds16(base + (((8 + 2 * g) ^ sw) << 4));
+            a[m][3] = lds16(base + (((9 + 2 * g) ^ sw) << 4));
+        }
+#pragma unroll
+        for (int n = 0; n < 4; ++n) {
+            const int brow = wn * 64 + n * 16 + r;
+            const uint8_t* base = sB + brow * BLK;
+            const int sw = swz8(brow);
+            const v4i lo = lds16(base + ((g ^ sw) << 4));
+            const v4i hi = lds16(base + (((g + 4) ^ sw) << 4));
+            const v4i b0 = fp8x8_to_bf16x8((uint32_t)lo.x, (uint32_t)lo.y);
+            const v4i b1 = fp8x8_to_bf16x8((uint32_t)lo.z, (uint32_t)lo.w);
+            const v4i b2 = fp8x8_to_bf16x8((uint32_t)hi.x, (uint32_t)hi.y);
+            const v4i b3 = fp8x8_to_bf16x8((uint32_t)hi.z, (uint32_t)hi.w);
+#pragma unroll
+            for (int m = 0; m < 4; ++m) {
+                v4f pr = zero;
+                pr = mfma_bf16_16x16x32(__builtin_bit_cast(v8bf, a[m][0]), __builtin_bit_cast(v8bf, b0), pr);
+                pr = mfma_bf16_16x16x32(__builtin_bit_cast(v8bf, a[m][1]), __builtin_bit_cast(v8bf, b1), pr);
+                pr = mfma_bf16_16x16x32(__builtin_bit_cast(v8bf, a[m][2]), __builtin_bit_cast(v8bf, b2), pr);
+                pr = mfma_bf16_16x16x32(__builtin_bit_cast(v8bf, a[m][3]), __builtin_bit_cast(v8bf, b3), pr);
+                acc[m][n][0] += pr[0] * sb;
+                acc[m][n][1] += pr[1] * sb;
+                acc[m][n][2] += pr[2] * sb;
+                acc[m][n][3] += pr[3] * sb;
+            }
+        }
+        wait_vmem();
+        __syncthreads();
+    }
+
+#pragma unroll
+    for (int m = 0; m < 4; ++m) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int row = wm * 64 + m * 16 + g * 4 + i;
+            if (row < nrows) {
+                float* dst = p.part + (size_t)(row0 + row) * H + n0 + wn * 64 + r;
+#pragma unroll
+                for (int n = 0; n < 4; ++n) dst[n * 16] = acc[m][n][i];
+            }
+        }
+    }
+}
+
+hipError_t launch_gemm2_tile(const Plan& p, const uint8_t* w2, const float* w2s, int variant,
+                             hipStream_t s) {
+    if (variant == 3) {
+        using C = G2Tile<2, 4>;
+        const int tiles = max_mtiles(p.T, C::BM) * C::NT;
+        dim3 grid((tiles + 7) / 8 * 8);
+        hipLaunchKernelGGL((gemm2_tile_kernel<2, 4, 4>), grid, dim3(C::THREADS), 0, s, p, w2, w2s);
+    } else {
+        using C = G2Tile<1, 4>;
+        const int tiles = max_mtiles(p.T, C::BM) * C::NT;
+        dim3 grid((tiles + 7) / 8 * 8);
+        hipLaunchKernelGGL((gemm2_tile_kernel<1, 4, 4>), grid, dim3(C::THREADS), 0, s, p, w2, w2s);
+    }
+    return hipGetLastError();
+}
+
+}  // namespace mimoe

@@ -1,0 +1,66 @@
+// Helpers shared by the LDS-tiled GEMM kernels (prefill shapes).
+#pragma once
+
+#include "common.hpp"
+
+namespace mimoe {
+
+typedef __attribute__((address_space(3))) void* lds_ptr_t;
+
+// 16-byte global -> LDS copy: lane l's 16 bytes land at lds_base + 16 * l
+// (lds_base must be wave-uniform; gfx950 global_load_lds_dwordx4).
+__device__ __forceinline__ void g2l16(const void* gsrc, void* lds_base) {
+    __builtin_amdgcn_global_load_lds(gsrc, (lds_ptr_t)lds_base, 16, 0, 0);
+}
+
+// 4-byte global -> LDS copy: lane l's dword lands at lds_base + 4 * l.
+__device__ __forceinline__ void g2l4(const void* gsrc, void* lds_base) {
+    __builtin_amdgcn_global_load_lds(gsrc, (lds_ptr_t)lds_base, 4, 0, 0);
+}
+
+__device__ __forceinline__ void wait_vmem() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
+
+// XOR swizzle of the 16-byte chunk index inside a 128-byte LDS row: 16
+// consecutive rows reading the same logical chunk hit 16 distinct 16-byte
+// bank groups (conflict-free for 32- and 64-bank LDS).
+__device__ __forceinline__ int swz8(int row) { return (row & 7) ^ ((row >> 3) & 1); }
+
+// Same for a 256-byte row of 16 chunks.
+__device__ __forceinline__ int swz16(int row) { return row & 15; }
+
+__device__ __forceinline__ v4i lds16(const uint8_t* p) { return *reinterpret_cast<const v4i*>(p); }
+
+// Logical tile order shared by the tiled GEMMs. Tiles of one expert are
+// visited in groups of GM row tiles; inside a group every n tile is swept
+// with the GM row tiles innermost, so the tiles running at the same time
+// on one XCD share weight and activation tiles in that XCD's L2. Each XCD
+// (workgroup b runs on XCD b % 8) takes one contiguous eighth of the order.
+template <int NT, int GM>
+__device__ __forceinline__ bool tile_coords(const int* meta, int mtile_base, int bm, int& e,
+                                            int& row0, int& nrows, int& nt) {
+    const int total = meta[mtile_base + EL] * NT;
+    const int per_xcd = (total + 7) >> 3;
+    const int b = blockIdx.x;
+    const int idx = b >> 3;
+    if (idx >= per_xcd) return false;
+    const int t = (b & 7) * per_xcd + idx;
+    if (t >= total) return false;
+    const int mt = t / NT;  // NT tiles per row tile: find the expert by row-tile index
+    int ee = 0;
+#pragma unroll
+    for (int k = 0; k < EL; ++k) ee += (meta[mtile_base + k + 1] <= mt) ? 1 : 0;
+    e = ee;
+    const int mt0 = meta[mtile_base + ee];
+    const int mts = meta[mtile_base + ee + 1] - mt0;  // row tiles of this expert
+    const int u = t - mt0 * NT;                        // tile index inside the expert
+    const int grp = u / (GM * NT);
+    const int gm = min(GM, mts - grp * GM);            // row tiles in this group
+    const int v = u - grp * GM * NT;
+    nt = v / gm;
+    const int mtl = grp * GM + (v - nt * gm);
+    row0 = meta[META_EXPERT_OFF + ee] + mtl * bm;
+    nrows = min(bm, meta[META_EXPERT_OFF + ee + 1] - row0);
+    return true;
+}
+
+}  // namespace mimoe

@@ -192,3 +192,15 @@ def test_scalar_tensor_arguments():
     kernel.run(*args, out)
     torch.cuda.synchronize()
     assert torch.equal(a.view(torch.int16), out.view(torch.int16))
+
+
+@pytest.mark.parametrize("variant", ["0", "1", "2", "3", "4", "0,3", "3,0"])
+@pytest.mark.parametrize("name", ["c1_t64", "c2_t1024_o128"])
+def test_every_gemm_variant_matches_oracle(name, variant, monkeypatch):
+    """Each GEMM kernel family (weight-streaming with 16/32/64-row tiles, LDS
+    tiles of two sizes, and mixes) gives the same answer within the bar."""
+    log(f"test_every_gemm_variant_matches_oracle[{name}-{variant}]")
+    monkeypatch.setenv("MI_MOE_VARIANT", variant)
+    wl = W.standard(name)
+    out = run_gpu(wl, fill=float("nan"))
+    _check_output(wl, out, spread_tokens(wl.T, 96))
