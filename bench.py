@@ -9,9 +9,9 @@ decode sweep's T=64 point (H=7168, I=2048, 32 local experts of 256, top-8,
 FP8 e4m3 block-scaled), which streams the active experts' weights and is
 bound by HBM bandwidth. W untimed calls, then 5 trials of K calls each,
 bracketed by ``torch.cuda.synchronize()``; ``value`` is the median trial's
-microseconds per call. Every call records HIP events between its five
-kernels on the stream they run on, which gives each kernel's average
-duration over the timed region.
+microseconds per call. A second pass of 5 x K calls records HIP events
+between the five kernels on the stream they run on, which gives each
+kernel's average duration.
 
 Rank 0 prints ONE JSON line. ``roofline`` covers the dominant kernel
 (GEMM1+SwiGLU at decode); ``call_roofline`` the whole call; ``sweep`` the
@@ -65,8 +65,6 @@ def gemm2_bytes(S, A_e):
 
 def make(name):
     from flashinfer_amd import workloads as W
-    if name == "t256":
-        return W.make_workload("t256", T=256, seed=111, local_expert_offset=0)
     return W.standard(name)
 
 
@@ -102,17 +100,28 @@ def time_workload(wl, steps, warmup, trials=5):
         kernel.run(*args, out)
     torch.cuda.synchronize()
     S, A_e, max_rows = routing_stats(wl.T)
+    # value: plain calls, trials x steps, bracketed by synchronize
+    trial_us = []
+    for tr in range(trials):
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for k in range(steps):
+            kernel.run(*args, out)
+        torch.cuda.synchronize()
+        trial_us.append((time.perf_counter() - t0) * 1e6 / steps)
+    # per-kernel durations: the same calls with HIP events recorded between the
+    # kernels on their stream (the records add a little time between kernels)
     nev = _lib.NUM_PHASES + 1
     ev = [[torch.cuda.Event(enable_timing=True) for _ in range(nev)] for _ in range(steps)]
-    trial_us = []
     phase_sum = [0.0] * _lib.NUM_PHASES
+    prof_us = []
     for tr in range(trials):
         torch.cuda.synchronize()
         t0 = time.perf_counter()
         for k in range(steps):
             kernel.run_profiled(*args, out, events=ev[k])
         torch.cuda.synchronize()
-        trial_us.append((time.perf_counter() - t0) * 1e6 / steps)
+        prof_us.append((time.perf_counter() - t0) * 1e6 / steps)
         for k in range(steps):
             for p in range(_lib.NUM_PHASES):
                 phase_sum[p] += ev[k][p].elapsed_time(ev[k][p + 1]) * 1e3
@@ -127,6 +136,7 @@ def time_workload(wl, steps, warmup, trials=5):
         "workload": wl.name, "T": wl.T, "local_expert_offset": wl.local_expert_offset,
         "slots": S, "active_experts": A_e, "max_rows_per_expert": max_rows,
         "us_per_call": round(us, 2), "trials_us": [round(x, 2) for x in trial_us],
+        "us_per_call_with_phase_events": round(statistics.median(prof_us), 2),
         "gbps": round(B / t / 1e9, 1), "tflops": round(F / t / 1e12, 2),
         "hbm_frac": round(B / t / 1e9 / HBM_PEAK_GBS, 4),
         "fp8_frac": round(F / t / 1e12 / FP8_PEAK_TFLOPS, 4),

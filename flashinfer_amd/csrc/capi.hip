@@ -64,7 +64,7 @@ struct Variants {
 
 Variants pick_variants(int64_t T) {
     Variants v;
-    if (T <= 128) v = {0, 0};
+    if (T <= 128) v = {5, 0};
     else if (T <= 1024) v = {1, 1};
     else if (T <= 2048) v = {4, 4};
     else v = {3, 3};
@@ -201,9 +201,17 @@ static int run_impl(const mi_moe_args* a, hipStream_t s, hipEvent_t const* ev) {
         err = launch_gemm1(p, a->hidden_states, a->hidden_states_scale, a->gemm1_weights,
                            a->gemm1_weights_scale, var.g1, s);
     mark(3);
-    if (err == hipSuccess) err = launch_gemm2(p, a->gemm2_weights, a->gemm2_weights_scale, var.g2, s);
+    const bool fused = var.g2 == VARIANT_GEMM2_COMBINE && gemm2_combine_supported(p.T);
+    if (err == hipSuccess) {
+        if (fused)
+            err = launch_gemm2_combine(p, a->gemm2_weights, a->gemm2_weights_scale,
+                                       (uint16_t*)a->output, s);
+        else
+            err = launch_gemm2(p, a->gemm2_weights, a->gemm2_weights_scale,
+                               var.g2 == VARIANT_GEMM2_COMBINE ? 0 : var.g2, s);
+    }
     mark(4);
-    if (err == hipSuccess) err = launch_combine(p, (uint16_t*)a->output, s);
+    if (err == hipSuccess && !fused) err = launch_combine(p, (uint16_t*)a->output, s);
     mark(5);
     if (err != hipSuccess)
         return fail(MI_MOE_ERR_HIP, "mi_moe_run: launch failed: %s", hipGetErrorString(err));

@@ -12,36 +12,42 @@
 
 namespace mimoe {
 
+// Grid (T, H / 1024): one workgroup per token and 1024-column chunk; each
+// thread owns 4 columns and issues the loads of all its <= 8 slot rows
+// before summing them, so a call costs about one memory round trip.
 __global__ __launch_bounds__(256) void combine_kernel(Plan p, uint16_t* __restrict__ out) {
     const int t = blockIdx.x;
+    const int c = blockIdx.y * 1024 + threadIdx.x * 4;
     const int4 s0 = reinterpret_cast<const int4*>(p.tok_slot + (size_t)t * TOPK)[0];
     const int4 s1 = reinterpret_cast<const int4*>(p.tok_slot + (size_t)t * TOPK)[1];
     const int slot[8] = {s0.x, s0.y, s0.z, s0.w, s1.x, s1.y, s1.z, s1.w};
     float w[8];
+    float4 v[8];
 #pragma unroll
-    for (int j = 0; j < TOPK; ++j) w[j] = slot[j] >= 0 ? p.sorted_w[slot[j]] : 0.f;
-
-    for (int c = threadIdx.x * 4; c < H; c += 256 * 4) {
-        float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
-#pragma unroll
-        for (int j = 0; j < TOPK; ++j) {
-            if (slot[j] < 0) break;
-            const float4 v = *reinterpret_cast<const float4*>(p.part + (size_t)slot[j] * H + c);
-            acc.x += w[j] * v.x;
-            acc.y += w[j] * v.y;
-            acc.z += w[j] * v.z;
-            acc.w += w[j] * v.w;
-        }
-        uint2 o;
-        o.x = (uint32_t)f2bf(acc.x) | ((uint32_t)f2bf(acc.y) << 16);
-        o.y = (uint32_t)f2bf(acc.z) | ((uint32_t)f2bf(acc.w) << 16);
-        *reinterpret_cast<uint2*>(out + (size_t)t * H + c) = o;
+    for (int j = 0; j < TOPK; ++j) {
+        const bool ok = slot[j] >= 0;
+        w[j] = ok ? p.sorted_w[slot[j]] : 0.f;
+        v[j] = ok ? *reinterpret_cast<const float4*>(p.part + (size_t)slot[j] * H + c)
+                  : make_float4(0.f, 0.f, 0.f, 0.f);
     }
+    float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+    for (int j = 0; j < TOPK; ++j) {
+        if (slot[j] < 0) break;
+        acc.x += w[j] * v[j].x;
+        acc.y += w[j] * v[j].y;
+        acc.z += w[j] * v[j].z;
+        acc.w += w[j] * v[j].w;
+    }
+    uint2 o;
+    o.x = (uint32_t)f2bf(acc.x) | ((uint32_t)f2bf(acc.y) << 16);
+    o.y = (uint32_t)f2bf(acc.z) | ((uint32_t)f2bf(acc.w) << 16);
+    *reinterpret_cast<uint2*>(out + (size_t)t * H + c) = o;
 }
 
 hipError_t launch_combine(const Plan& p, uint16_t* out, hipStream_t s) {
     if (p.T <= 0) return hipSuccess;
-    hipLaunchKernelGGL(combine_kernel, dim3(p.T), dim3(256), 0, s, p, out);
+    hipLaunchKernelGGL(combine_kernel, dim3(p.T, H / 1024), dim3(256), 0, s, p, out);
     return hipGetLastError();
 }
 

@@ -130,6 +130,9 @@ hipError_t launch_gemm1(const Plan& p, const uint8_t* hs, const float* hs_scale,
 hipError_t launch_gemm2(const Plan& p, const uint8_t* w2, const float* w2s, int variant,
                         hipStream_t s);
 hipError_t launch_combine(const Plan& p, uint16_t* out, hipStream_t s);
+bool gemm2_combine_supported(int T);
+hipError_t launch_gemm2_combine(const Plan& p, const uint8_t* w2, const float* w2s, uint16_t* out,
+                                hipStream_t s);
 hipError_t launch_gemm1_tile(const Plan& p, const uint8_t* hs, const float* hs_scale,
                              const uint8_t* w1, const float* w1s, int variant, hipStream_t s);
 hipError_t launch_gemm2_tile(const Plan& p, const uint8_t* w2, const float* w2s, int variant,
@@ -138,7 +141,9 @@ hipError_t launch_gemm2_tile(const Plan& p, const uint8_t* w2, const float* w2s,
 // GEMM kernel variants: 0/1/2 weight-streaming with 16/32/64-row tiles,
 // 3 LDS-tiled large (GEMM1 256 rows, GEMM2 128 rows), 4 LDS-tiled medium
 // (GEMM1 128 rows, GEMM2 64 rows).
-constexpr int NUM_VARIANTS = 5;
+constexpr int NUM_VARIANTS = 11;
+// GEMM2 variant that also performs the combine (decode sizes only).
+constexpr int VARIANT_GEMM2_COMBINE = 10;
 
 // Row-tile height of each GEMM variant (rows of one expert per workgroup).
 int gemm1_bm(int variant);

@@ -22,15 +22,14 @@
 
 namespace mimoe {
 
-template <int MT, int D>
-__global__ __launch_bounds__(256) void gemm1_stream_kernel(Plan p, const uint8_t* __restrict__ hs,
-                                                           const float* __restrict__ hs_scale,
-                                                           const uint8_t* __restrict__ w1,
-                                                           const float* __restrict__ w1s) {
+template <int MT, int D, int NW>
+__global__ __launch_bounds__(64 * NW) void gemm1_stream_kernel(Plan p, const uint8_t* __restrict__ hs,
+                                                               const float* __restrict__ hs_scale,
+                                                               const uint8_t* __restrict__ w1,
+                                                               const float* __restrict__ w1s) {
     static_assert(HB % D == 0, "prefetch depth must divide the k-block count");
     constexpr int BM = 16 * MT;
     __shared__ float sa_lds[HB][BM];
-    __shared__ int tok_lds[BM];
 
     int e, row0, nrows;
     if (!find_tile(p.meta, META_MTILE1, blockIdx.y, BM, e, row0, nrows)) return;
@@ -38,21 +37,14 @@ __global__ __launch_bounds__(256) void gemm1_stream_kernel(Plan p, const uint8_t
     const int tid = threadIdx.x;
     const int lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-    if (tid < BM) tok_lds[tid] = p.sorted_tok[row0 + min(tid, nrows - 1)];
-    __syncthreads();
-    for (int i = tid; i < HB * BM; i += 256) {
-        const int kb = i / BM, m = i % BM;
-        sa_lds[kb][m] = hs_scale[(size_t)kb * p.T + tok_lds[m]];
-    }
-    __syncthreads();
-
-    const int j0 = blockIdx.x * 64 + wave * 16;
+    const int j0 = blockIdx.x * (16 * NW) + wave * 16;
     const int r = lane & 15, g = lane >> 4;
     const uint8_t* bg_ptr = w1 + ((size_t)e * N1 + j0 + r) * H + g * 16;
     const uint8_t* bu_ptr = w1 + ((size_t)e * N1 + I + j0 + r) * H + g * 16;
     const uint8_t* a_ptr[MT];
 #pragma unroll
-    for (int i = 0; i < MT; ++i) a_ptr[i] = hs + (size_t)tok_lds[i * 16 + r] * H + g * 16;
+    for (int i = 0; i < MT; ++i)
+        a_ptr[i] = hs + (size_t)p.sorted_tok[row0 + min(i * 16 + r, nrows - 1)] * H + g * 16;
     const float* sbg_ptr = w1s + ((size_t)e * N1B + j0 / BLK) * HB;
     const float* sbu_ptr = w1s + ((size_t)e * N1B + (I + j0) / BLK) * HB;
 
@@ -90,8 +82,15 @@ __global__ __launch_bounds__(256) void gemm1_stream_kernel(Plan p, const uint8_t
         for (int i = 0; i < MT; ++i) a[d][i] = ld_frag(a_ptr[i] + nk);
     };
 
+    // Start streaming weights first; the activation scales of the tile go to
+    // LDS while those loads are in flight.
 #pragma unroll
     for (int d = 0; d < D; ++d) load(d, d);
+    for (int i = tid; i < HB * BM; i += 64 * NW) {
+        const int kb = i / BM, m = i % BM;
+        sa_lds[kb][m] = hs_scale[(size_t)kb * p.T + p.sorted_tok[row0 + min(m, nrows - 1)]];
+    }
+    __syncthreads();
 
     // Steady state: every stage is refilled right after it is consumed.
 #pragma unroll 1
@@ -125,29 +124,32 @@ int gemm1_bm(int variant) {
         case 1: return 32;
         case 2: return 64;
         case 3: return 256;
-        default: return 128;
+        case 4: return 128;
+        default: return 16;
     }
+}
+
+template <int MT, int D, int NW>
+static void launch_stream1(const Plan& p, const uint8_t* hs, const float* hs_scale,
+                           const uint8_t* w1, const float* w1s, hipStream_t s) {
+    dim3 grid(I / (16 * NW), max_mtiles(p.T, 16 * MT));
+    hipLaunchKernelGGL((gemm1_stream_kernel<MT, D, NW>), grid, dim3(64 * NW), 0, s, p, hs,
+                       hs_scale, w1, w1s);
 }
 
 hipError_t launch_gemm1(const Plan& p, const uint8_t* hs, const float* hs_scale, const uint8_t* w1,
                         const float* w1s, int variant, hipStream_t s) {
     if (p.T <= 0) return hipSuccess;
-    if (variant >= 3) return launch_gemm1_tile(p, hs, hs_scale, w1, w1s, variant, s);
-    const int bm = gemm1_bm(variant);
-    dim3 grid(I / 64, max_mtiles(p.T, bm));
+    if (variant >= 3 && variant <= 4) return launch_gemm1_tile(p, hs, hs_scale, w1, w1s, variant, s);
     switch (variant) {
-        case 0:
-            hipLaunchKernelGGL((gemm1_stream_kernel<1, 4>), grid, dim3(256), 0, s, p, hs, hs_scale,
-                               w1, w1s);
-            break;
-        case 1:
-            hipLaunchKernelGGL((gemm1_stream_kernel<2, 4>), grid, dim3(256), 0, s, p, hs, hs_scale,
-                               w1, w1s);
-            break;
-        default:
-            hipLaunchKernelGGL((gemm1_stream_kernel<4, 2>), grid, dim3(256), 0, s, p, hs, hs_scale,
-                               w1, w1s);
-            break;
+        case 0: launch_stream1<1, 4, 4>(p, hs, hs_scale, w1, w1s, s); break;
+        case 1: launch_stream1<2, 4, 4>(p, hs, hs_scale, w1, w1s, s); break;
+        case 2: launch_stream1<4, 2, 4>(p, hs, hs_scale, w1, w1s, s); break;
+        case 5: launch_stream1<1, 4, 1>(p, hs, hs_scale, w1, w1s, s); break;
+        case 6: launch_stream1<1, 8, 1>(p, hs, hs_scale, w1, w1s, s); break;
+        case 7: launch_stream1<1, 8, 4>(p, hs, hs_scale, w1, w1s, s); break;
+        case 8: launch_stream1<1, 4, 2>(p, hs, hs_scale, w1, w1s, s); break;
+        default: launch_stream1<1, 2, 1>(p, hs, hs_scale, w1, w1s, s); break;
     }
     return hipGetLastError();
 }

@@ -135,14 +135,15 @@ int gemm2_bm(int variant) {
         case 1: return 32;
         case 2: return 64;
         case 3: return 128;
-        default: return 64;
+        case 4: return 64;
+        default: return 16;
     }
 }
 
 hipError_t launch_gemm2(const Plan& p, const uint8_t* w2, const float* w2s, int variant,
                         hipStream_t s) {
     if (p.T <= 0) return hipSuccess;
-    if (variant >= 3) return launch_gemm2_tile(p, w2, w2s, variant, s);
+    if (variant >= 3 && variant <= 4) return launch_gemm2_tile(p, w2, w2s, variant, s);
     const int bm = gemm2_bm(variant);
     dim3 grid(HB, max_mtiles(p.T, bm));
     switch (variant) {
@@ -152,8 +153,11 @@ hipError_t launch_gemm2(const Plan& p, const uint8_t* w2, const float* w2s, int 
         case 1:
             hipLaunchKernelGGL((gemm2_stream_kernel<2, 4>), grid, dim3(256), 0, s, p, w2, w2s);
             break;
-        default:
+        case 2:
             hipLaunchKernelGGL((gemm2_stream_kernel<4, 2>), grid, dim3(256), 0, s, p, w2, w2s);
+            break;
+        default:
+            hipLaunchKernelGGL((gemm2_stream_kernel<1, 8>), grid, dim3(256), 0, s, p, w2, w2s);
             break;
     }
     return hipGetLastError();

@@ -10,9 +10,11 @@
 // (:442-452) is applied later by the sort kernel, so this kernel writes the
 // global ids, which also serve the routing-parity check.
 //
-// Lane l of the wave owns experts 4l..4l+3, so one routing group is 8 lanes
-// and every reduction is a short butterfly inside the wave: no LDS, no
-// barriers, one 1 KB coalesced load of logits per token.
+// Lane l of the wave owns experts 4l..4l+3, so one routing group is 8 lanes.
+// Reductions use DPP lane exchanges (a few cycles each) and readlane, not
+// LDS permutes: the group top-2 is three DPP merges, and each of the 8
+// top-k rounds is one 4-step DPP max, 4 readlanes and a ballot for the
+// lowest index. No LDS, no barriers, one 1 KB coalesced load per token.
 #include "common.hpp"
 
 namespace mimoe {
@@ -24,6 +26,42 @@ __device__ __forceinline__ uint32_t ord_f32(float f) {
 }
 
 __device__ __forceinline__ float sigmoid_f32(float x) { return 1.0f / (1.0f + expf(-x)); }
+
+// DPP lane exchanges (gfx9 encodings): xor 1 / xor 2 inside a quad, mirror
+// inside each 8-lane half row, mirror inside each 16-lane row.
+constexpr int DPP_XOR1 = 0xB1;         // quad_perm [1,0,3,2]
+constexpr int DPP_XOR2 = 0x4E;         // quad_perm [2,3,0,1]
+constexpr int DPP_HALF_MIRROR = 0x141;
+constexpr int DPP_MIRROR = 0x140;
+
+template <int CTRL>
+__device__ __forceinline__ uint32_t dpp_u(uint32_t v) {
+    return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, CTRL, 0xF, 0xF, false);
+}
+template <int CTRL>
+__device__ __forceinline__ float dpp_f(float v) {
+    return __builtin_bit_cast(float, dpp_u<CTRL>(__builtin_bit_cast(uint32_t, v)));
+}
+
+__device__ __forceinline__ void top2_merge(float& m1, float& m2, float o1, float o2) {
+    const float n1 = fmaxf(m1, o1);
+    const float n2 = fmaxf(fminf(m1, o1), fmaxf(m2, o2));
+    m1 = n1;
+    m2 = n2;
+}
+
+// Largest key of the wave, returned in every lane (uniform).
+__device__ __forceinline__ uint32_t wave_max_u32(uint32_t k) {
+    k = max(k, dpp_u<DPP_XOR1>(k));
+    k = max(k, dpp_u<DPP_XOR2>(k));
+    k = max(k, dpp_u<DPP_HALF_MIRROR>(k));
+    k = max(k, dpp_u<DPP_MIRROR>(k));  // every lane now holds its 16-lane row's max
+    const uint32_t r0 = __builtin_amdgcn_readlane(k, 0);
+    const uint32_t r1 = __builtin_amdgcn_readlane(k, 16);
+    const uint32_t r2 = __builtin_amdgcn_readlane(k, 32);
+    const uint32_t r3 = __builtin_amdgcn_readlane(k, 48);
+    return max(max(r0, r1), max(r2, r3));
+}
 
 __global__ __launch_bounds__(256) void route_kernel(const float* __restrict__ logits,
                                                     const void* __restrict__ bias, int bias_is_f32,
@@ -43,8 +81,8 @@ __global__ __launch_bounds__(256) void route_kernel(const float* __restrict__ lo
         b0 = bf2f(raw.x & 0xffffu); b1 = bf2f(raw.x >> 16);
         b2 = bf2f(raw.y & 0xffffu); b3 = bf2f(raw.y >> 16);
     }
-    float s[4] = {sigmoid_f32(x.x), sigmoid_f32(x.y), sigmoid_f32(x.z), sigmoid_f32(x.w)};
-    float sb[4] = {s[0] + b0, s[1] + b1, s[2] + b2, s[3] + b3};
+    const float s[4] = {sigmoid_f32(x.x), sigmoid_f32(x.y), sigmoid_f32(x.z), sigmoid_f32(x.w)};
+    const float sb[4] = {s[0] + b0, s[1] + b1, s[2] + b2, s[3] + b3};
 
     // Top-2 (as a multiset) of the lane's 4 values, then of the 8-lane group.
     float m1 = fmaxf(sb[0], sb[1]), m2 = fminf(sb[0], sb[1]);
@@ -53,57 +91,47 @@ __global__ __launch_bounds__(256) void route_kernel(const float* __restrict__ lo
         const float v = sb[j];
         if (v > m1) { m2 = m1; m1 = v; } else { m2 = fmaxf(m2, v); }
     }
-#pragma unroll
-    for (int off = 1; off < 8; off <<= 1) {
-        const float o1 = __shfl_xor(m1, off);
-        const float o2 = __shfl_xor(m2, off);
-        const float n1 = fmaxf(m1, o1);
-        const float n2 = fmaxf(fminf(m1, o1), fmaxf(m2, o2));
-        m1 = n1; m2 = n2;
-    }
-    const float gscore = m1 + m2;
+    top2_merge(m1, m2, dpp_f<DPP_XOR1>(m1), dpp_f<DPP_XOR1>(m2));
+    top2_merge(m1, m2, dpp_f<DPP_XOR2>(m1), dpp_f<DPP_XOR2>(m2));
+    top2_merge(m1, m2, dpp_f<DPP_HALF_MIRROR>(m1), dpp_f<DPP_HALF_MIRROR>(m2));
+    const float gscore = m1 + m2;  // identical in the 8 lanes of the group
 
     // Rank of this lane's group among the 8 (lower index wins ties).
     const int my_g = lane >> 3;
     int rank = 0;
 #pragma unroll
     for (int h = 0; h < NGROUP; ++h) {
-        const float gh = __shfl(gscore, h * 8);
+        const float gh = __builtin_bit_cast(
+            float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, gscore), h * 8));
         rank += (gh > gscore) || (gh == gscore && h < my_g);
     }
     const bool gsel = rank < KGROUP;
 
-    // 64-bit keys: ordered score in the high word, (255 - id) in the low word,
-    // so one max picks the best score and, on ties, the lowest id.
-    unsigned long long key[4];
+    // Candidate keys: order-preserving image of s+bias; 0 = not a candidate
+    // (ord_f32 maps every non-NaN float, -inf included, above 0).
+    uint32_t key[4];
 #pragma unroll
-    for (int j = 0; j < 4; ++j)
-        key[j] = gsel ? (((unsigned long long)ord_f32(sb[j]) << 32) |
-                         (unsigned long long)(uint32_t)(255 - (lane * 4 + j)))
-                      : 0ull;
+    for (int j = 0; j < 4; ++j) key[j] = gsel ? ord_f32(sb[j]) : 0u;
 
     int ids[TOPK];
     float ss[TOPK];
 #pragma unroll
     for (int k = 0; k < TOPK; ++k) {
-        unsigned long long best = key[0];
+        const uint32_t local = max(max(key[0], key[1]), max(key[2], key[3]));
+        const uint32_t best = wave_max_u32(local);
+        // Lowest expert index holding the best key: lowest lane, then lowest j.
+        const unsigned long long holders = __ballot(local == best);
+        const int owner = __builtin_ctzll(holders);
+        const int jj = key[0] == best ? 0 : (key[1] == best ? 1 : (key[2] == best ? 2 : 3));
+        const int j_owner = __builtin_amdgcn_readlane(jj, owner);
+        const float sv = j_owner == 0 ? s[0] : (j_owner == 1 ? s[1] : (j_owner == 2 ? s[2] : s[3]));
+        ss[k] = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, sv), owner));
+        ids[k] = owner * 4 + j_owner;
+        if (lane == owner) {
 #pragma unroll
-        for (int j = 1; j < 4; ++j) best = key[j] > best ? key[j] : best;
-#pragma unroll
-        for (int off = 32; off > 0; off >>= 1) {
-            const unsigned long long o = __shfl_xor(best, off);
-            best = o > best ? o : best;
+            for (int j = 0; j < 4; ++j)
+                if (j == j_owner) key[j] = 0u;
         }
-        const int idx = 255 - (int)(uint32_t)(best & 0xffffffffull);
-        const int owner = idx >> 2;
-        const int jj = idx & 3;
-#pragma unroll
-        for (int j = 0; j < 4; ++j)
-            if (lane == owner && j == jj) key[j] = 0ull;
-        float sv = jj == 0 ? s[0] : (jj == 1 ? s[1] : (jj == 2 ? s[2] : s[3]));
-        sv = __shfl(sv, owner);
-        ids[k] = idx;
-        ss[k] = sv;
     }
     float denom = ss[0];
 #pragma unroll

@@ -41,21 +41,27 @@ __global__ __launch_bounds__(1024) void sort_kernel(Plan p, int bm1, int bm2) {
         }
     }
     __syncthreads();
-    if (tid == 0) {
-        int acc = 0, a1 = 0, a2 = 0;
-        for (int e = 0; e < EL; ++e) {
-            p.meta[META_EXPERT_OFF + e] = acc;
-            p.meta[META_MTILE1 + e] = a1;
-            p.meta[META_MTILE2 + e] = a2;
-            base[e] = acc;
-            const int c = cnt[e];
-            acc += c;
-            a1 += (c + bm1 - 1) / bm1;
-            a2 += (c + bm2 - 1) / bm2;
+    if (tid < 64) {
+        // Exclusive prefix of slot counts and of row tiles, 32 lanes in parallel.
+        const int c = tid < EL ? cnt[tid] : 0;
+        int v0 = c, v1 = (c + bm1 - 1) / bm1, v2 = (c + bm2 - 1) / bm2;
+        const int own0 = v0, own1 = v1, own2 = v2;
+#pragma unroll
+        for (int d = 1; d < EL; d <<= 1) {
+            const int u0 = __shfl_up(v0, d), u1 = __shfl_up(v1, d), u2 = __shfl_up(v2, d);
+            if (tid >= d) { v0 += u0; v1 += u1; v2 += u2; }
         }
-        p.meta[META_EXPERT_OFF + EL] = acc;
-        p.meta[META_MTILE1 + EL] = a1;
-        p.meta[META_MTILE2 + EL] = a2;
+        if (tid < EL) {
+            p.meta[META_EXPERT_OFF + tid] = v0 - own0;
+            p.meta[META_MTILE1 + tid] = v1 - own1;
+            p.meta[META_MTILE2 + tid] = v2 - own2;
+            base[tid] = v0 - own0;
+            if (tid == EL - 1) {
+                p.meta[META_EXPERT_OFF + EL] = v0;
+                p.meta[META_MTILE1 + EL] = v1;
+                p.meta[META_MTILE2 + EL] = v2;
+            }
+        }
     }
     __syncthreads();
 

@@ -102,6 +102,7 @@ STANDARD = {
     "c1_t4": dict(T=4, seed=102, local_expert_offset=0),
     "c1_t16": dict(T=16, seed=103, local_expert_offset=0),
     "c1_t64": dict(T=64, seed=104, local_expert_offset=0),
+    "t256": dict(T=256, seed=111, local_expert_offset=0),
     "c2_t1024_o0": dict(T=1024, seed=105, local_expert_offset=0),
     "c2_t1024_o64": dict(T=1024, seed=106, local_expert_offset=64),
     "c2_t1024_o128": dict(T=1024, seed=107, local_expert_offset=128),

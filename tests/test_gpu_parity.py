@@ -64,7 +64,7 @@ def _check_output(wl, out, tokens):
     return rep
 
 
-@pytest.mark.parametrize("name", ["c1_t1", "c1_t4", "c0_t16", "c1_t16", "c1_t64"])
+@pytest.mark.parametrize("name", ["c1_t1", "c1_t4", "c0_t16", "c1_t16", "c1_t64", "t256"])
 def test_output_parity_decode(name):
     log(f"test_output_parity_decode[{name}]")
     wl = W.standard(name)
@@ -194,8 +194,9 @@ def test_scalar_tensor_arguments():
     assert torch.equal(a.view(torch.int16), out.view(torch.int16))
 
 
-@pytest.mark.parametrize("variant", ["0", "1", "2", "3", "4", "0,3", "3,0"])
-@pytest.mark.parametrize("name", ["c1_t64", "c2_t1024_o128"])
+@pytest.mark.parametrize("variant", ["0", "1", "2", "3", "4", "0,3", "3,0", "5,10", "6,10", "7,1",
+                                     "8,2", "9,10", "1,10"])
+@pytest.mark.parametrize("name", ["c1_t64", "t256", "c2_t1024_o128"])
 def test_every_gemm_variant_matches_oracle(name, variant, monkeypatch):
     """Each GEMM kernel family (weight-streaming with 16/32/64-row tiles, LDS
     tiles of two sizes, and mixes) gives the same answer within the bar."""
