@@ -54,7 +54,7 @@ class MiMoeArgs(ctypes.Structure):
 class MiMoeLayout(ctypes.Structure):
     _fields_ = [(n, ctypes.c_size_t) for n in
                 ("topk_ids", "topk_w", "expert_off", "sorted_tok", "sorted_w", "tok_slot",
-                 "act", "part", "total")]
+                 "chunk_cnt", "act", "part", "total")]
 
 
 _lib = None

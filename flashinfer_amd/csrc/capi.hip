@@ -48,6 +48,7 @@ mi_moe_layout make_layout(int64_t T) {
     L.sorted_tok = o; o = align_up(o + s_max * 4);
     L.sorted_w = o;   o = align_up(o + s_max * 4);
     L.tok_slot = o;   o = align_up(o + t * TOPK * 4);
+    L.chunk_cnt = o;  o = align_up(o + (size_t)sort_chunks((int)t) * EL * 4);
     L.act = o;        o = align_up(o + s_max * I * 2);
     L.part = o;       o = align_up(o + s_max * H * 4);
     L.total = o;
@@ -62,11 +63,18 @@ struct Variants {
     int g1, g2;
 };
 
+// Routing and sort as one launch for small T (MI_MOE_FUSE_FRONT=0/1 overrides).
+bool fuse_front_end(int64_t T) {
+    bool f = T <= 8;
+    const char* env = getenv("MI_MOE_FUSE_FRONT");
+    if (env && *env) f = atoi(env) != 0;
+    return f && route_sort_supported((int)T);
+}
+
 Variants pick_variants(int64_t T) {
     Variants v;
     if (T <= 128) v = {5, 0};
-    else if (T <= 1024) v = {1, 1};
-    else if (T <= 2048) v = {4, 4};
+    else if (T <= 256) v = {1, 1};
     else v = {3, 3};
     const char* env = getenv("MI_MOE_VARIANT");
     if (env && *env) {
@@ -182,6 +190,7 @@ static int run_impl(const mi_moe_args* a, hipStream_t s, hipEvent_t const* ev) {
     p.sorted_tok = (int*)(ws + L.sorted_tok);
     p.sorted_w = (float*)(ws + L.sorted_w);
     p.tok_slot = (int*)(ws + L.tok_slot);
+    p.chunk_cnt = (int*)(ws + L.chunk_cnt);
     p.act = (uint16_t*)(ws + L.act);
     p.part = (float*)(ws + L.part);
 
@@ -190,12 +199,20 @@ static int run_impl(const mi_moe_args* a, hipStream_t s, hipEvent_t const* ev) {
     auto mark = [&](int i) {
         if (ev && err == hipSuccess) err = hipEventRecord(ev[i], s);
     };
+    const int bias_f32 = a->bias_dtype == MI_MOE_DTYPE_F32;
     mark(0);
-    if (err == hipSuccess)
-        err = launch_route(a->routing_logits, a->routing_bias, a->bias_dtype == MI_MOE_DTYPE_F32,
-                           p.T, p.rsf, p.topk_ids, p.topk_w, s);
-    mark(1);
-    if (err == hipSuccess) err = launch_sort(p, gemm1_bm(var.g1), gemm2_bm(var.g2), s);
+    if (fuse_front_end(T)) {
+        if (err == hipSuccess)
+            err = launch_route_sort(p, a->routing_logits, a->routing_bias, bias_f32,
+                                    gemm1_bm(var.g1), gemm2_bm(var.g2), s);
+        mark(1);
+    } else {
+        if (err == hipSuccess)
+            err = launch_route(a->routing_logits, a->routing_bias, bias_f32, p.T, p.rsf,
+                               p.topk_ids, p.topk_w, s);
+        mark(1);
+        if (err == hipSuccess) err = launch_sort(p, gemm1_bm(var.g1), gemm2_bm(var.g2), s);
+    }
     mark(2);
     if (err == hipSuccess)
         err = launch_gemm1(p, a->hidden_states, a->hidden_states_scale, a->gemm1_weights,

@@ -33,6 +33,7 @@ struct Plan {
     int* sorted_tok;           // [8T]
     float* sorted_w;           // [8T]
     int* tok_slot;             // [T, 8]
+    int* chunk_cnt;            // [ceil(T/1024), 32] per-chunk expert totals (large-T sort)
     uint16_t* act;             // bf16 [8T, 2048]
     float* part;               // [8T, 7168]
 };
@@ -125,6 +126,11 @@ inline int max_mtiles(int T, int bm) {
 hipError_t launch_route(const float* logits, const void* bias, int bias_is_f32, int T, float rsf,
                         int* topk_ids, float* topk_w, hipStream_t s);
 hipError_t launch_sort(const Plan& p, int bm1, int bm2, hipStream_t s);
+// Routing + sort in one single-workgroup launch (small T only).
+bool route_sort_supported(int T);
+int sort_chunks(int T);
+hipError_t launch_route_sort(const Plan& p, const float* logits, const void* bias, int bias_is_f32,
+                             int bm1, int bm2, hipStream_t s);
 hipError_t launch_gemm1(const Plan& p, const uint8_t* hs, const float* hs_scale, const uint8_t* w1,
                         const float* w1s, int variant, hipStream_t s);
 hipError_t launch_gemm2(const Plan& p, const uint8_t* w2, const float* w2s, int variant,

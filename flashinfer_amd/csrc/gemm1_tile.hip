@@ -31,12 +31,13 @@ struct G1Tile {
     static constexpr int B_BYTES = 2 * BG * BLK;
     static constexpr int SA_BYTES = BM * 4;
     static constexpr int STAGE = A_BYTES + B_BYTES + SA_BYTES;
+    static constexpr int SCRATCH = 256 * NW;  // L2-prefetch landing area
     static constexpr int A_LD = A_BYTES / 1024 / NW;  // 1 KB copies per wave per stage
     static constexpr int B_LD = B_BYTES / 1024 / NW;
     static constexpr int SA_WAVES = BM / 64;          // waves copying one scale each per lane
     static_assert(A_BYTES % (1024 * NW) == 0 && B_BYTES % (1024 * NW) == 0, "loader split");
     static_assert(SA_WAVES <= NW, "scale loader");
-    static_assert(2 * STAGE <= 160 * 1024, "LDS budget");
+    static_assert(2 * STAGE + SCRATCH <= 160 * 1024, "LDS budget");
 };
 
 template <int WM, int WN, int GM>
@@ -44,7 +45,7 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm1_tile_kernel(
     Plan p, const uint8_t* __restrict__ hs, const float* __restrict__ hs_scale,
     const uint8_t* __restrict__ w1, const float* __restrict__ w1s) {
     using C = G1Tile<WM, WN>;
-    __shared__ __attribute__((aligned(1024))) uint8_t smem[2 * C::STAGE];
+    __shared__ __attribute__((aligned(1024))) uint8_t smem[2 * C::STAGE + C::SCRATCH];
 
     int e, row0, nrows, nt;
     if (!tile_coords<C::NT, GM>(p.meta, META_MTILE1, C::BM, e, row0, nrows, nt)) return;
@@ -70,6 +71,16 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm1_tile_kernel(
         const int c = (lane & 7) ^ swz8(row);
         const int wrow = row < C::BG ? jb + row : I + jb + (row - C::BG);
         b_off[i] = (uint32_t)((e * N1 + wrow) * H + c * 16);
+    }
+    // L2 prefetch of k-block kb+2: lanes 0..31 touch the wave's A rows, lanes
+    // 32..63 its B rows (one 128-byte line each).
+    const uint8_t* pf_base;
+    {
+        const int prow = C::BM / C::NW * wave + (lane & 31) % (C::BM / C::NW);
+        const int brow = (2 * C::BG) / C::NW * wave + (lane & 31) % ((2 * C::BG) / C::NW);
+        const int tok = p.sorted_tok[row0 + min(prow, nrows - 1)];
+        const int wrow = brow < C::BG ? jb + brow : I + jb + (brow - C::BG);
+        pf_base = lane < 32 ? hs + (size_t)tok * H : w1 + ((size_t)e * N1 + wrow) * H;
     }
     uint32_t sa_off = 0;
     if (wave < C::SA_WAVES) {
@@ -105,18 +116,19 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm1_tile_kernel(
     wait_vmem();
     __syncthreads();
 
+    uint8_t* pf_lds = smem + 2 * C::STAGE + 256 * wave;
+    prefetch_l2(pf_base + 1 * BLK, pf_lds);
+
 #pragma unroll 1
     for (int kb = 0; kb < HB; ++kb) {
         const int cur = kb & 1;
         if (kb + 1 < HB) issue(cur ^ 1, kb + 1);
+        prefetch_l2(pf_base + min(kb + 2, HB - 1) * BLK, pf_lds);
         const uint8_t* sA = smem + cur * C::STAGE;
         const uint8_t* sB = sA + C::A_BYTES;
         const float* sSA = reinterpret_cast<const float*>(sB + C::B_BYTES);
 
         v8i a[4];
-        float cg[4][4], cu[4][4];
-        const float sg = sbg_p[kb];
-        const float su = sbu_p[kb];
 #pragma unroll
         for (int m = 0; m < 4; ++m) {
             const int row = wm * 64 + m * 16 + r;
@@ -125,31 +137,50 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm1_tile_kernel(
             const v4i lo = lds16(base + ((g ^ sw) << 4));
             const v4i hi = lds16(base + (((g + 4) ^ sw) << 4));
             a[m] = (v8i){lo.x, lo.y, lo.z, lo.w, hi.x, hi.y, hi.z, hi.w};
-            const float4 s4 = *reinterpret_cast<const float4*>(sSA + wm * 64 + m * 16 + g * 4);
-            cg[m][0] = s4.x * sg; cg[m][1] = s4.y * sg; cg[m][2] = s4.z * sg; cg[m][3] = s4.w * sg;
-            cu[m][0] = s4.x * su; cu[m][1] = s4.y * su; cu[m][2] = s4.z * su; cu[m][3] = s4.w * su;
         }
+        // Per-row scale products sa*sb for the gate half, then (re-read from
+        // LDS) for the up half: one set of 16 registers instead of two.
+        float cs[4][4];
+        auto set_scales = [&](float sb) __attribute__((always_inline)) {
 #pragma unroll
-        for (int n = 0; n < 8; ++n) {
+            for (int m = 0; m < 4; ++m) {
+                const float4 s4 = *reinterpret_cast<const float4*>(sSA + wm * 64 + m * 16 + g * 4);
+                cs[m][0] = s4.x * sb; cs[m][1] = s4.y * sb; cs[m][2] = s4.z * sb; cs[m][3] = s4.w * sb;
+            }
+        };
+        // B fragments are read one column tile ahead so the LDS latency of
+        // tile n+1 overlaps the MFMAs of tile n.
+        auto read_b = [&](int n) __attribute__((always_inline)) {
             const int brow = (n < 4) ? (wn * 64 + n * 16 + r) : (C::BG + wn * 64 + (n - 4) * 16 + r);
             const uint8_t* base = sB + brow * BLK;
             const int sw = swz8(brow);
             const v4i lo = lds16(base + ((g ^ sw) << 4));
             const v4i hi = lds16(base + (((g + 4) ^ sw) << 4));
-            const v8i b = (v8i){lo.x, lo.y, lo.z, lo.w, hi.x, hi.y, hi.z, hi.w};
+            return (v8i){lo.x, lo.y, lo.z, lo.w, hi.x, hi.y, hi.z, hi.w};
+        };
+        set_scales(sbg_p[kb]);
+        v8i bnext = read_b(0);
+#pragma unroll
+        for (int n = 0; n < 8; ++n) {
+            if (n == 4) set_scales(sbu_p[kb]);
+            const v8i b = bnext;
+            if (n < 7) bnext = read_b(n + 1);
+            // four independent MFMAs, then their scale-and-accumulate
+            v4f pr[4];
+#pragma unroll
+            for (int m = 0; m < 4; ++m) pr[m] = mfma_f8_16x16x128(a[m], b, zero);
 #pragma unroll
             for (int m = 0; m < 4; ++m) {
-                const v4f pr = mfma_f8_16x16x128(a[m], b, zero);
-                const float* sc = (n < 4) ? cg[m] : cu[m];
-                acc[m][n][0] += pr[0] * sc[0];
-                acc[m][n][1] += pr[1] * sc[1];
-                acc[m][n][2] += pr[2] * sc[2];
-                acc[m][n][3] += pr[3] * sc[3];
+                acc[m][n][0] += pr[m][0] * cs[m][0];
+                acc[m][n][1] += pr[m][1] * cs[m][1];
+                acc[m][n][2] += pr[m][2] * cs[m][2];
+                acc[m][n][3] += pr[m][3] * cs[m][3];
             }
         }
-        wait_vmem();
+        wait_vmem_but_one();
         __syncthreads();
     }
+    wait_vmem();
 
 #pragma unroll
     for (int m = 0; m < 4; ++m) {

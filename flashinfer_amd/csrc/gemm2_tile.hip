@@ -126,17 +126,27 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm2_tile_kernel(Plan p,
             const v4i b1 = fp8x8_to_bf16x8((uint32_t)lo.z, (uint32_t)lo.w);
             const v4i b2 = fp8x8_to_bf16x8((uint32_t)hi.x, (uint32_t)hi.y);
             const v4i b3 = fp8x8_to_bf16x8((uint32_t)hi.z, (uint32_t)hi.w);
+            // the four row tiles' k-chains interleaved: consecutive MFMAs are
+            // independent, then one scale-and-accumulate per row tile
+            v4f pr[4] = {zero, zero, zero, zero};
+#pragma unroll
+            for (int m = 0; m < 4; ++m)
+                pr[m] = mfma_bf16_16x16x32(__builtin_bit_cast(v8bf, a[m][0]), __builtin_bit_cast(v8bf, b0), pr[m]);
+#pragma unroll
+            for (int m = 0; m < 4; ++m)
+                pr[m] = mfma_bf16_16x16x32(__builtin_bit_cast(v8bf, a[m][1]), __builtin_bit_cast(v8bf, b1), pr[m]);
+#pragma unroll
+            for (int m = 0; m < 4; ++m)
+                pr[m] = mfma_bf16_16x16x32(__builtin_bit_cast(v8bf, a[m][2]), __builtin_bit_cast(v8bf, b2), pr[m]);
+#pragma unroll
+            for (int m = 0; m < 4; ++m)
+                pr[m] = mfma_bf16_16x16x32(__builtin_bit_cast(v8bf, a[m][3]), __builtin_bit_cast(v8bf, b3), pr[m]);
 #pragma unroll
             for (int m = 0; m < 4; ++m) {
-                v4f pr = zero;
-                pr = mfma_bf16_16x16x32(__builtin_bit_cast(v8bf, a[m][0]), __builtin_bit_cast(v8bf, b0), pr);
-                pr = mfma_bf16_16x16x32(__builtin_bit_cast(v8bf, a[m][1]), __builtin_bit_cast(v8bf, b1), pr);
-                pr = mfma_bf16_16x16x32(__builtin_bit_cast(v8bf, a[m][2]), __builtin_bit_cast(v8bf, b2), pr);
-                pr = mfma_bf16_16x16x32(__builtin_bit_cast(v8bf, a[m][3]), __builtin_bit_cast(v8bf, b3), pr);
-                acc[m][n][0] += pr[0] * sb;
-                acc[m][n][1] += pr[1] * sb;
-                acc[m][n][2] += pr[2] * sb;
-                acc[m][n][3] += pr[3] * sb;
+                acc[m][n][0] += pr[m][0] * sb;
+                acc[m][n][1] += pr[m][1] * sb;
+                acc[m][n][2] += pr[m][2] * sb;
+                acc[m][n][3] += pr[m][3] * sb;
             }
         }
         wait_vmem();

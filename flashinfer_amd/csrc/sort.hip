@@ -1,4 +1,4 @@
-// Local-expert histogram, prefix sum and stable permute in one workgroup.
+// Local-expert histogram, prefix sum and stable permute.
 //
 // Replaces solution/triton/kernel.py:460-505 (_count_local_experts_kernel,
 // _scatter_local_tokens_kernel), the host-synchronising scan at :572-581 and
@@ -10,128 +10,276 @@
 //   * it also writes, per token, its slots in ascending local-expert order,
 //     which the combine kernel walks instead of scattering with atomics.
 //
-// Placement works per chunk of 1024 tokens: each wave counts its 64 tokens'
-// hits per expert with one ballot per expert, the 16 wave counts are scanned
-// in LDS, and a lane's slot is chunk base + wave prefix + popcount of the
-// lower lanes' ballot bits.
-#include "common.hpp"
+// Placement works per chunk of 1024 tokens (one per thread): each wave counts
+// its 64 tokens' hits per expert with one ballot per expert, the 16 wave
+// counts are scanned in LDS, and a lane's slot is chunk base + wave prefix +
+// popcount of the lower lanes' ballot bits.
+//
+// Three entry shapes: one workgroup for T <= 1024 (sort_kernel); the same
+// with the routing done in place for small T (route_sort_kernel, one launch
+// for the whole front end); and for large T a per-chunk count kernel plus a
+// per-chunk place kernel that scans the chunk totals itself.
+#include "route_impl.hpp"
 
 namespace mimoe {
 
-__global__ __launch_bounds__(1024) void sort_kernel(Plan p, int bm1, int bm2) {
-    __shared__ int cnt[EL];
-    __shared__ int base[EL];
-    __shared__ int wcnt[16][EL];
-    const int tid = threadIdx.x;
-    const int lane = tid & 63;
-    const int wave = tid >> 6;
-    const int T = p.T;
-    const int off = p.local_offset;
+constexpr int CHUNK = 1024;
 
-    if (tid < EL) cnt[tid] = 0;
-    __syncthreads();
-    for (int t = tid; t < T; t += 1024) {
-        const int4 i0 = reinterpret_cast<const int4*>(p.topk_ids + (size_t)t * TOPK)[0];
-        const int4 i1 = reinterpret_cast<const int4*>(p.topk_ids + (size_t)t * TOPK)[1];
-        const int ids[8] = {i0.x, i0.y, i0.z, i0.w, i1.x, i1.y, i1.z, i1.w};
+// A token's local experts: bit mask over the 32 local ids, and per top-k
+// position the local id (-1 if not local) and routing weight.
+struct TokLocal {
+    uint32_t m;
+    int lid[TOPK];
+    float lw[TOPK];
+};
+
+__device__ __forceinline__ TokLocal make_local(const int ids[TOPK], const float ws[TOPK], int off) {
+    TokLocal r;
+    r.m = 0;
 #pragma unroll
-        for (int k = 0; k < TOPK; ++k) {
-            const int l = ids[k] - off;
-            if ((unsigned)l < (unsigned)EL) atomicAdd(&cnt[l], 1);
+    for (int k = 0; k < TOPK; ++k) {
+        const int l = ids[k] - off;
+        const bool loc = (unsigned)l < (unsigned)EL;
+        r.lid[k] = loc ? l : -1;
+        r.lw[k] = ws[k];
+        r.m |= loc ? (1u << l) : 0u;
+    }
+    return r;
+}
+
+__device__ __forceinline__ TokLocal load_local(const int* ids_base, const float* w_base, int t,
+                                               bool valid, int off) {
+    int ids[TOPK];
+    float ws[TOPK];
+    if (valid) {
+        const int4 i0 = reinterpret_cast<const int4*>(ids_base + (size_t)t * TOPK)[0];
+        const int4 i1 = reinterpret_cast<const int4*>(ids_base + (size_t)t * TOPK)[1];
+        const float4 w0 = reinterpret_cast<const float4*>(w_base + (size_t)t * TOPK)[0];
+        const float4 w1 = reinterpret_cast<const float4*>(w_base + (size_t)t * TOPK)[1];
+        ids[0] = i0.x; ids[1] = i0.y; ids[2] = i0.z; ids[3] = i0.w;
+        ids[4] = i1.x; ids[5] = i1.y; ids[6] = i1.z; ids[7] = i1.w;
+        ws[0] = w0.x; ws[1] = w0.y; ws[2] = w0.z; ws[3] = w0.w;
+        ws[4] = w1.x; ws[5] = w1.y; ws[6] = w1.z; ws[7] = w1.w;
+    } else {
+#pragma unroll
+        for (int k = 0; k < TOPK; ++k) { ids[k] = -1 - EL; ws[k] = 0.f; }  // never local
+    }
+    return make_local(ids, ws, valid ? off : 0);
+}
+
+// Exclusive prefix of the per-expert slot counts held by lanes 0..31 of the
+// calling wave (every lane of the wave must call). Optionally writes the
+// expert offsets and the row-tile prefixes for GEMM tiles of bm1 / bm2 rows.
+__device__ __forceinline__ int scan_counts(const Plan& p, int lane, int c, int bm1, int bm2,
+                                           bool write) {
+    int v0 = c, v1 = (c + bm1 - 1) / bm1, v2 = (c + bm2 - 1) / bm2;
+    const int own0 = v0, own1 = v1, own2 = v2;
+#pragma unroll
+    for (int d = 1; d < EL; d <<= 1) {
+        const int u0 = __shfl_up(v0, d), u1 = __shfl_up(v1, d), u2 = __shfl_up(v2, d);
+        if (lane >= d) { v0 += u0; v1 += u1; v2 += u2; }
+    }
+    if (write && lane < EL) {
+        p.meta[META_EXPERT_OFF + lane] = v0 - own0;
+        p.meta[META_MTILE1 + lane] = v1 - own1;
+        p.meta[META_MTILE2 + lane] = v2 - own2;
+        if (lane == EL - 1) {
+            p.meta[META_EXPERT_OFF + EL] = v0;
+            p.meta[META_MTILE1 + EL] = v1;
+            p.meta[META_MTILE2 + EL] = v2;
         }
     }
-    __syncthreads();
-    if (tid < 64) {
-        // Exclusive prefix of slot counts and of row tiles, 32 lanes in parallel.
-        const int c = tid < EL ? cnt[tid] : 0;
-        int v0 = c, v1 = (c + bm1 - 1) / bm1, v2 = (c + bm2 - 1) / bm2;
-        const int own0 = v0, own1 = v1, own2 = v2;
-#pragma unroll
-        for (int d = 1; d < EL; d <<= 1) {
-            const int u0 = __shfl_up(v0, d), u1 = __shfl_up(v1, d), u2 = __shfl_up(v2, d);
-            if (tid >= d) { v0 += u0; v1 += u1; v2 += u2; }
-        }
-        if (tid < EL) {
-            p.meta[META_EXPERT_OFF + tid] = v0 - own0;
-            p.meta[META_MTILE1 + tid] = v1 - own1;
-            p.meta[META_MTILE2 + tid] = v2 - own2;
-            base[tid] = v0 - own0;
-            if (tid == EL - 1) {
-                p.meta[META_EXPERT_OFF + EL] = v0;
-                p.meta[META_MTILE1 + EL] = v1;
-                p.meta[META_MTILE2 + EL] = v2;
-            }
-        }
-    }
-    __syncthreads();
+    return v0 - own0;
+}
 
+// Per-wave hit counts of the chunk into wcnt[wave][e] (lane e writes).
+__device__ __forceinline__ void wave_counts(const TokLocal& tl, int lane, int wave,
+                                            int (*wcnt)[EL]) {
+#pragma unroll
+    for (int e = 0; e < EL; ++e) {
+        const unsigned long long bal = __ballot((tl.m >> e) & 1u);
+        if (lane == e) wcnt[wave][e] = __popcll(bal);
+    }
+}
+
+// Writes the slots of one chunk given wcnt[wave][e] = first slot of expert e
+// for the wave's tokens (every thread of the workgroup calls it).
+__device__ __forceinline__ void place_with_prefix(const Plan& p, int t, bool valid,
+                                                  const TokLocal& tl, int (*wcnt)[EL], int lane,
+                                                  int wave) {
     const unsigned long long lower = (1ull << lane) - 1ull;
-    for (int c0 = 0; c0 < T; c0 += 1024) {
-        const int t = c0 + tid;
-        const bool valid = t < T;
-        int lid[TOPK];
-        float lw[TOPK];
-        uint32_t m = 0;
-        if (valid) {
-            const int4 i0 = reinterpret_cast<const int4*>(p.topk_ids + (size_t)t * TOPK)[0];
-            const int4 i1 = reinterpret_cast<const int4*>(p.topk_ids + (size_t)t * TOPK)[1];
-            const float4 w0 = reinterpret_cast<const float4*>(p.topk_w + (size_t)t * TOPK)[0];
-            const float4 w1 = reinterpret_cast<const float4*>(p.topk_w + (size_t)t * TOPK)[1];
-            const int ids[8] = {i0.x, i0.y, i0.z, i0.w, i1.x, i1.y, i1.z, i1.w};
-            const float ws[8] = {w0.x, w0.y, w0.z, w0.w, w1.x, w1.y, w1.z, w1.w};
+    int j = 0;
 #pragma unroll
-            for (int k = 0; k < TOPK; ++k) {
-                const int l = ids[k] - off;
-                const bool loc = (unsigned)l < (unsigned)EL;
-                lid[k] = loc ? l : -1;
-                lw[k] = ws[k];
-                m |= loc ? (1u << l) : 0u;
-            }
-        } else {
+    for (int e = 0; e < EL; ++e) {
+        const bool hit = (tl.m >> e) & 1u;
+        const unsigned long long bal = __ballot(hit);
+        if (hit) {
+            const int pos = wcnt[wave][e] + __popcll(bal & lower);
+            float w = 0.f;
 #pragma unroll
-            for (int k = 0; k < TOPK; ++k) { lid[k] = -1; lw[k] = 0.f; }
+            for (int k = 0; k < TOPK; ++k) w = (tl.lid[k] == e) ? tl.lw[k] : w;
+            p.sorted_tok[pos] = t;
+            p.sorted_w[pos] = w;
+            p.tok_slot[(size_t)t * TOPK + j] = pos;
+            ++j;
         }
-#pragma unroll
-        for (int e = 0; e < EL; ++e) {
-            const unsigned long long bal = __ballot((m >> e) & 1u);
-            if (lane == e) wcnt[wave][e] = __popcll(bal);
+    }
+    if (valid)
+        for (; j < TOPK; ++j) p.tok_slot[(size_t)t * TOPK + j] = -1;
+}
+
+// Places one chunk (every thread of the 1024-thread workgroup calls it).
+// base[e] holds the chunk's first slot for expert e.
+__device__ void place_chunk(const Plan& p, int t, bool valid, const TokLocal& tl, const int* base,
+                            int (*wcnt)[EL], int tid, int lane, int wave) {
+    wave_counts(tl, lane, wave, wcnt);
+    __syncthreads();
+    if (tid < EL) {
+        int run = base[tid];
+        for (int w = 0; w < CHUNK / 64; ++w) {
+            const int c = wcnt[w][tid];
+            wcnt[w][tid] = run;
+            run += c;
         }
-        __syncthreads();
-        if (tid < EL) {
-            int run = base[tid];
-            for (int w = 0; w < 16; ++w) {
-                const int c = wcnt[w][tid];
-                wcnt[w][tid] = run;
+    }
+    __syncthreads();
+    place_with_prefix(p, t, valid, tl, wcnt, lane, wave);
+}
+
+// Counts, scan and placement for T <= CHUNK in one workgroup, reading each
+// token's top-k once from ids_base / w_base (global or LDS): the per-wave
+// ballot counts give both the expert totals and the wave prefixes.
+__device__ void sort_one_workgroup(const Plan& p, const int* ids_base, const float* w_base, int bm1,
+                                   int bm2, int (*wcnt)[EL]) {
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const bool valid = tid < p.T;
+    const TokLocal tl = load_local(ids_base, w_base, tid, valid, p.local_offset);
+    wave_counts(tl, lane, wave, wcnt);
+    __syncthreads();
+    if (wave == 0) {
+        int total = 0;
+        if (lane < EL)
+            for (int w = 0; w < CHUNK / 64; ++w) total += wcnt[w][lane];
+        const int off = scan_counts(p, lane, total, bm1, bm2, true);
+        if (lane < EL) {
+            int run = off;
+            for (int w = 0; w < CHUNK / 64; ++w) {
+                const int c = wcnt[w][lane];
+                wcnt[w][lane] = run;
                 run += c;
             }
-            base[tid] = run;
         }
-        __syncthreads();
-        int j = 0;
-#pragma unroll
-        for (int e = 0; e < EL; ++e) {
-            const bool hit = (m >> e) & 1u;
-            const unsigned long long bal = __ballot(hit);
-            if (hit) {
-                const int pos = wcnt[wave][e] + __popcll(bal & lower);
-                float w = 0.f;
-#pragma unroll
-                for (int k = 0; k < TOPK; ++k) w = (lid[k] == e) ? lw[k] : w;
-                p.sorted_tok[pos] = t;
-                p.sorted_w[pos] = w;
-                p.tok_slot[(size_t)t * TOPK + j] = pos;
-                ++j;
+    }
+    __syncthreads();
+    place_with_prefix(p, tid, valid, tl, wcnt, lane, wave);
+}
+
+__global__ __launch_bounds__(1024) void sort_kernel(Plan p, int bm1, int bm2) {
+    __shared__ int wcnt[CHUNK / 64][EL];
+    sort_one_workgroup(p, p.topk_ids, p.topk_w, bm1, bm2, wcnt);
+}
+
+// Routing + sort in one launch for small T: the 16 waves route the tokens
+// round-robin (global top-k also written for parity checks), then sort from
+// the LDS copy.
+constexpr int ROUTE_SORT_MAX_T = 256;
+
+__global__ __launch_bounds__(1024) void route_sort_kernel(Plan p, const float* __restrict__ logits,
+                                                          const void* __restrict__ bias,
+                                                          int bias_is_f32, int bm1, int bm2) {
+    __shared__ int wcnt[CHUNK / 64][EL];
+    __shared__ __attribute__((aligned(16))) int s_ids[ROUTE_SORT_MAX_T * TOPK];
+    __shared__ __attribute__((aligned(16))) float s_w[ROUTE_SORT_MAX_T * TOPK];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    for (int t = wave; t < p.T; t += CHUNK / 64) {
+        int ids[TOPK];
+        float w[TOPK];
+        route_token(logits + (size_t)t * EG, bias, bias_is_f32, p.rsf, lane, ids, w);
+        if (lane == 0) {
+            const int4 i0 = make_int4(ids[0], ids[1], ids[2], ids[3]);
+            const int4 i1 = make_int4(ids[4], ids[5], ids[6], ids[7]);
+            const float4 w0 = make_float4(w[0], w[1], w[2], w[3]);
+            const float4 w1 = make_float4(w[4], w[5], w[6], w[7]);
+            reinterpret_cast<int4*>(p.topk_ids + (size_t)t * TOPK)[0] = i0;
+            reinterpret_cast<int4*>(p.topk_ids + (size_t)t * TOPK)[1] = i1;
+            reinterpret_cast<float4*>(p.topk_w + (size_t)t * TOPK)[0] = w0;
+            reinterpret_cast<float4*>(p.topk_w + (size_t)t * TOPK)[1] = w1;
+            reinterpret_cast<int4*>(s_ids + t * TOPK)[0] = i0;
+            reinterpret_cast<int4*>(s_ids + t * TOPK)[1] = i1;
+            reinterpret_cast<float4*>(s_w + t * TOPK)[0] = w0;
+            reinterpret_cast<float4*>(s_w + t * TOPK)[1] = w1;
+        }
+    }
+    __syncthreads();
+    sort_one_workgroup(p, s_ids, s_w, bm1, bm2, wcnt);
+}
+
+// Large T, pass 1: per-chunk expert totals into chunk_cnt[chunk][32].
+__global__ __launch_bounds__(1024) void sort_count_kernel(Plan p) {
+    __shared__ int wcnt[CHUNK / 64][EL];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int t = blockIdx.x * CHUNK + tid;
+    const bool valid = t < p.T;
+    const TokLocal tl = load_local(p.topk_ids, p.topk_w, t, valid, p.local_offset);
+    wave_counts(tl, lane, wave, wcnt);
+    __syncthreads();
+    if (tid < EL) {
+        int s = 0;
+        for (int w = 0; w < CHUNK / 64; ++w) s += wcnt[w][tid];
+        p.chunk_cnt[blockIdx.x * EL + tid] = s;
+    }
+}
+
+// Large T, pass 2: each chunk derives its per-expert base from the chunk
+// totals (chunk 0 also writes the expert offsets and tile prefixes), then
+// places its tokens.
+__global__ __launch_bounds__(1024) void sort_place_kernel(Plan p, int nchunks, int bm1, int bm2) {
+    __shared__ int base[EL];
+    __shared__ int wcnt[CHUNK / 64][EL];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int cb = blockIdx.x;
+    if (wave == 0) {
+        int before = 0, total = 0;
+        if (lane < EL) {
+            for (int c = 0; c < nchunks; ++c) {
+                const int v = p.chunk_cnt[c * EL + lane];
+                before += c < cb ? v : 0;
+                total += v;
             }
         }
-        if (valid)
-            for (; j < TOPK; ++j) p.tok_slot[(size_t)t * TOPK + j] = -1;
-        __syncthreads();
+        const int off = scan_counts(p, lane, total, bm1, bm2, cb == 0);
+        if (lane < EL) base[lane] = off + before;
     }
+    __syncthreads();
+    const int t = cb * CHUNK + tid;
+    const bool valid = t < p.T;
+    const TokLocal tl = load_local(p.topk_ids, p.topk_w, t, valid, p.local_offset);
+    place_chunk(p, t, valid, tl, base, wcnt, tid, lane, wave);
+}
+
+bool route_sort_supported(int T) { return T > 0 && T <= ROUTE_SORT_MAX_T; }
+
+int sort_chunks(int T) { return (T + CHUNK - 1) / CHUNK; }
+
+hipError_t launch_route_sort(const Plan& p, const float* logits, const void* bias, int bias_is_f32,
+                             int bm1, int bm2, hipStream_t s) {
+    if (p.T <= 0) return hipSuccess;
+    hipLaunchKernelGGL(route_sort_kernel, dim3(1), dim3(CHUNK), 0, s, p, logits, bias, bias_is_f32,
+                       bm1, bm2);
+    return hipGetLastError();
 }
 
 hipError_t launch_sort(const Plan& p, int bm1, int bm2, hipStream_t s) {
     if (p.T <= 0) return hipSuccess;
-    hipLaunchKernelGGL(sort_kernel, dim3(1), dim3(1024), 0, s, p, bm1, bm2);
+    const int nchunks = sort_chunks(p.T);
+    if (nchunks == 1) {
+        hipLaunchKernelGGL(sort_kernel, dim3(1), dim3(CHUNK), 0, s, p, bm1, bm2);
+        return hipGetLastError();
+    }
+    hipLaunchKernelGGL(sort_count_kernel, dim3(nchunks), dim3(CHUNK), 0, s, p);
+    hipError_t err = hipGetLastError();
+    if (err != hipSuccess) return err;
+    hipLaunchKernelGGL(sort_place_kernel, dim3(nchunks), dim3(CHUNK), 0, s, p, nchunks, bm1, bm2);
     return hipGetLastError();
 }
 

@@ -7,18 +7,48 @@ namespace mimoe {
 
 typedef __attribute__((address_space(3))) void* lds_ptr_t;
 
+// LDS byte address of a pointer into __shared__ memory.
+__device__ __forceinline__ uint32_t lds_addr(const void* p) {
+    return (uint32_t)(size_t)(lds_ptr_t)p;
+}
+
 // 16-byte global -> LDS copy: lane l's 16 bytes land at lds_base + 16 * l
 // (lds_base must be wave-uniform; gfx950 global_load_lds_dwordx4).
+//
+// Written as inline asm on purpose: the compiler cannot tell that a copy into
+// one LDS stage does not alias reads of the other stage, and would put a
+// vmcnt(0) wait in front of every LDS read, serialising copy and compute.
+// The kernels using these place their own vmcnt waits before each barrier.
+// One wait state between the M0 write and the LDS DMA is required.
 __device__ __forceinline__ void g2l16(const void* gsrc, void* lds_base) {
-    __builtin_amdgcn_global_load_lds(gsrc, (lds_ptr_t)lds_base, 16, 0, 0);
+    asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off"
+                 :
+                 : "v"(gsrc), "s"(lds_addr(lds_base))
+                 : "memory", "m0");
 }
 
 // 4-byte global -> LDS copy: lane l's dword lands at lds_base + 4 * l.
 __device__ __forceinline__ void g2l4(const void* gsrc, void* lds_base) {
-    __builtin_amdgcn_global_load_lds(gsrc, (lds_ptr_t)lds_base, 4, 0, 0);
+    asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dword %0, off"
+                 :
+                 : "v"(gsrc), "s"(lds_addr(lds_base))
+                 : "memory", "m0");
 }
 
 __device__ __forceinline__ void wait_vmem() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
+
+// Waits for all but the most recent vector-memory load (loads return in
+// order), leaving one L2 prefetch in flight.
+__device__ __forceinline__ void wait_vmem_but_one() {
+    asm volatile("s_waitcnt vmcnt(1)" ::: "memory");
+}
+
+// L2 prefetch: a 4-byte LDS-DMA load of one cache line per lane into a
+// per-wave scratch area of 256 bytes in LDS (no VGPR is written), so that a
+// later copy of the line hits L2. Issue it after the copies it must not delay.
+__device__ __forceinline__ void prefetch_l2(const void* gsrc, void* lds_scratch) {
+    g2l4(gsrc, lds_scratch);
+}
 
 // XOR swizzle of the 16-byte chunk index inside a 128-byte LDS row: 16
 // consecutive rows reading the same logical chunk hit 16 distinct 16-byte

@@ -64,10 +64,11 @@ typedef struct mi_moe_args {
  *   sorted_tok int32 [8T]     token of each slot, expert-major, token-ascending
  *   sorted_w   fp32  [8T]     routing weight of each slot
  *   tok_slot   int32 [T, 8]   slots of each token, ascending local expert, -1 pad
+ *   chunk_cnt  int32 [ceil(T/1024), 32]  per-1024-token-chunk local expert counts
  *   act        bf16  [8T, 2048]  SwiGLU(GEMM1) per slot
  *   part       fp32  [8T, 7168]  GEMM2 per slot (unweighted)               */
 typedef struct mi_moe_layout {
-    size_t topk_ids, topk_w, expert_off, sorted_tok, sorted_w, tok_slot, act, part;
+    size_t topk_ids, topk_w, expert_off, sorted_tok, sorted_w, tok_slot, chunk_cnt, act, part;
     size_t total;
 } mi_moe_layout;
 

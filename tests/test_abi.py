@@ -35,7 +35,8 @@ def test_workspace_layout_monotone_and_aligned():
     prev = 0
     for T in (1, 2, 16, 64, 1024, 8192, 14000):
         L = _lib.workspace_layout(T)
-        offs = [L.topk_ids, L.topk_w, L.expert_off, L.sorted_tok, L.sorted_w, L.tok_slot, L.act, L.part]
+        offs = [L.topk_ids, L.topk_w, L.expert_off, L.sorted_tok, L.sorted_w, L.tok_slot,
+                L.chunk_cnt, L.act, L.part]
         assert offs == sorted(offs)
         assert all(o % 256 == 0 for o in offs)
         assert L.total == _lib.workspace_size(T) and L.total > prev
