@@ -50,7 +50,7 @@ mi_moe_layout make_layout(int64_t T) {
     L.tok_slot = o;   o = align_up(o + t * TOPK * 4);
     L.chunk_cnt = o;  o = align_up(o + (size_t)sort_chunks((int)t) * EL * 4);
     L.act = o;        o = align_up(o + s_max * I * 2);
-    L.part = o;       o = align_up(o + s_max * H * 4);
+    L.part = o;       o = align_up(o + s_max * H * 2);
     L.total = o;
     return L;
 }
@@ -73,7 +73,7 @@ bool fuse_front_end(int64_t T) {
 
 Variants pick_variants(int64_t T) {
     Variants v;
-    if (T <= 128) v = {5, 0};
+    if (T <= 128) v = {5, 5};
     else if (T <= 256) v = {1, 1};
     else v = {3, 3};
     const char* env = getenv("MI_MOE_VARIANT");
@@ -192,7 +192,7 @@ static int run_impl(const mi_moe_args* a, hipStream_t s, hipEvent_t const* ev) {
     p.tok_slot = (int*)(ws + L.tok_slot);
     p.chunk_cnt = (int*)(ws + L.chunk_cnt);
     p.act = (uint16_t*)(ws + L.act);
-    p.part = (float*)(ws + L.part);
+    p.part = (uint16_t*)(ws + L.part);
 
     const Variants var = pick_variants(T);
     hipError_t err = hipSuccess;

@@ -35,7 +35,7 @@ struct Plan {
     int* tok_slot;             // [T, 8]
     int* chunk_cnt;            // [ceil(T/1024), 32] per-chunk expert totals (large-T sort)
     uint16_t* act;             // bf16 [8T, 2048]
-    float* part;               // [8T, 7168]
+    uint16_t* part;            // bf16 [8T, 7168]: routing weight x GEMM2 row of each slot
 };
 
 constexpr int META_EXPERT_OFF = 0;
@@ -144,10 +144,12 @@ hipError_t launch_gemm1_tile(const Plan& p, const uint8_t* hs, const float* hs_s
 hipError_t launch_gemm2_tile(const Plan& p, const uint8_t* w2, const float* w2s, int variant,
                              hipStream_t s);
 
-// GEMM kernel variants: 0/1/2 weight-streaming with 16/32/64-row tiles,
-// 3 LDS-tiled large (GEMM1 256 rows, GEMM2 128 rows), 4 LDS-tiled medium
-// (GEMM1 128 rows, GEMM2 64 rows).
-constexpr int NUM_VARIANTS = 11;
+// GEMM kernel variants: 0/1/2 weight-streaming with 16/32/64-row tiles and
+// 4-wave workgroups, 3 LDS-tiled large (GEMM1 256 rows, GEMM2 128 rows),
+// 4 LDS-tiled medium (GEMM1 128 rows, GEMM2 64 rows), 5..12 weight-streaming
+// shapes with 1- or 2-wave workgroups (see the launchers), 10 GEMM2 fused
+// with the combine.
+constexpr int NUM_VARIANTS = 13;
 // GEMM2 variant that also performs the combine (decode sizes only).
 constexpr int VARIANT_GEMM2_COMBINE = 10;
 

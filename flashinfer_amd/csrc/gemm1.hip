@@ -125,6 +125,8 @@ int gemm1_bm(int variant) {
         case 2: return 64;
         case 3: return 256;
         case 4: return 128;
+        case 11: return 32;
+        case 12: return 32;
         default: return 16;
     }
 }
@@ -149,6 +151,8 @@ hipError_t launch_gemm1(const Plan& p, const uint8_t* hs, const float* hs_scale,
         case 6: launch_stream1<1, 8, 1>(p, hs, hs_scale, w1, w1s, s); break;
         case 7: launch_stream1<1, 8, 4>(p, hs, hs_scale, w1, w1s, s); break;
         case 8: launch_stream1<1, 4, 2>(p, hs, hs_scale, w1, w1s, s); break;
+        case 11: launch_stream1<2, 4, 1>(p, hs, hs_scale, w1, w1s, s); break;
+        case 12: launch_stream1<2, 2, 1>(p, hs, hs_scale, w1, w1s, s); break;
         default: launch_stream1<1, 2, 1>(p, hs, hs_scale, w1, w1s, s); break;
     }
     return hipGetLastError();

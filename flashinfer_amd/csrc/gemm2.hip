@@ -1,7 +1,8 @@
 // Grouped GEMM2 (down projection): FP8 weights, bf16 activations.
 //
 // Replaces solution/triton/kernel.py:193-293 (_persistent_gemm2_kernel):
-//   part[s, n] = sum_kb sb2[e, n/128, kb] * sum_{k in kb} act[s, k] * W2[e, n, k]
+//   part[s, n] = bf16(w_s * sum_kb sb2[e, n/128, kb] * sum_{k in kb} act[s, k] * W2[e, n, k])
+// (w_s = the slot's routing weight, applied here instead of in the combine)
 // The reference dequantises W2 to fp32 and runs an fp32 (TF32) dot
 // (:272-278). Here the fp8 weights are widened to bf16 in registers, which is
 // exact for e4m3, and fed with the bf16 SwiGLU output to
@@ -51,9 +52,10 @@ __device__ __forceinline__ v4f mfma_block(const Frag16& a, const v8i& b) {
     return acc;
 }
 
-template <int MT, int D>
-__global__ __launch_bounds__(256) void gemm2_stream_kernel(Plan p, const uint8_t* __restrict__ w2,
-                                                           const float* __restrict__ w2s) {
+template <int MT, int D, int NW, int NQ>
+__global__ __launch_bounds__(64 * NW) void gemm2_stream_kernel(Plan p, const uint8_t* __restrict__ w2,
+                                                               const float* __restrict__ w2s) {
+    static_assert(BLK % (16 * NQ) == 0, "a wave's columns stay inside one scale block");
     static_assert(IB % D == 0, "prefetch depth must divide the k-block count");
     constexpr int BM = 16 * MT;
     int e, row0, nrows;
@@ -62,24 +64,26 @@ __global__ __launch_bounds__(256) void gemm2_stream_kernel(Plan p, const uint8_t
     const int tid = threadIdx.x;
     const int lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const int nb = blockIdx.x;  // 128-column block of the output
-    const int n0 = nb * BLK + wave * 32;
+    const int n0 = blockIdx.x * (16 * NQ * NW) + wave * (16 * NQ);
+    const int nb = n0 / BLK;  // 128-column scale block of the wave's columns
     const int r = lane & 15, g = lane >> 4;
 
-    const uint8_t* b_ptr[2];
+    const uint8_t* b_ptr[NQ];
 #pragma unroll
-    for (int q = 0; q < 2; ++q) b_ptr[q] = w2 + ((size_t)e * H + n0 + q * 16 + r) * I + g * 16;
+    for (int q = 0; q < NQ; ++q) b_ptr[q] = w2 + ((size_t)e * H + n0 + q * 16 + r) * I + g * 16;
     const uint16_t* a_row[MT];
 #pragma unroll
     for (int i = 0; i < MT; ++i) a_row[i] = p.act + (size_t)(row0 + min(i * 16 + r, nrows - 1)) * I;
     const float* sb_ptr = w2s + ((size_t)e * HB + nb) * IB;
 
-    v8i b[D][2];
+    v8i b[D][NQ];
     Frag16 a[D][MT];
-    v4f acc[MT][2];
+    v4f acc[MT][NQ];
     const v4f zero = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-    for (int i = 0; i < MT; ++i) { acc[i][0] = zero; acc[i][1] = zero; }
+    for (int i = 0; i < MT; ++i)
+#pragma unroll
+        for (int q = 0; q < NQ; ++q) acc[i][q] = zero;
 
     auto compute = [&](int d, int kb) __attribute__((always_inline)) {
         const float sb = sb_ptr[kb];
@@ -97,7 +101,7 @@ __global__ __launch_bounds__(256) void gemm2_stream_kernel(Plan p, const uint8_t
     };
     auto load = [&](int d, int kb) __attribute__((always_inline)) {
 #pragma unroll
-        for (int q = 0; q < 2; ++q) b[d][q] = ld_frag(b_ptr[q] + kb * BLK);
+        for (int q = 0; q < NQ; ++q) b[d][q] = ld_frag(b_ptr[q] + kb * BLK);
 #pragma unroll
         for (int i = 0; i < MT; ++i) a[d][i] = ld_act(a_row[i], kb, g);
     };
@@ -115,15 +119,18 @@ __global__ __launch_bounds__(256) void gemm2_stream_kernel(Plan p, const uint8_t
 #pragma unroll
     for (int d = 0; d < D; ++d) compute(d, IB - D + d);
 
+    // Epilogue: weight each slot's row by its routing weight (kernel.py:364)
+    // and store bf16 for the combine.
 #pragma unroll
     for (int i = 0; i < MT; ++i) {
 #pragma unroll
         for (int rr = 0; rr < 4; ++rr) {
             const int m = i * 16 + g * 4 + rr;
             if (m < nrows) {
-                float* dst = p.part + (size_t)(row0 + m) * H + n0 + r;
-                dst[0] = acc[i][0][rr];
-                dst[16] = acc[i][1][rr];
+                const float w = p.sorted_w[row0 + m];
+                uint16_t* dst = p.part + (size_t)(row0 + m) * H + n0 + r;
+#pragma unroll
+                for (int q = 0; q < NQ; ++q) dst[16 * q] = f2bf(w * acc[i][q][rr]);
             }
         }
     }
@@ -136,29 +143,33 @@ int gemm2_bm(int variant) {
         case 2: return 64;
         case 3: return 128;
         case 4: return 64;
+        case 7: return 32;
+        case 12: return 32;
         default: return 16;
     }
+}
+
+template <int MT, int D, int NW, int NQ>
+static void launch_stream2(const Plan& p, const uint8_t* w2, const float* w2s, hipStream_t s) {
+    dim3 grid(H / (16 * NQ * NW), max_mtiles(p.T, 16 * MT));
+    hipLaunchKernelGGL((gemm2_stream_kernel<MT, D, NW, NQ>), grid, dim3(64 * NW), 0, s, p, w2, w2s);
 }
 
 hipError_t launch_gemm2(const Plan& p, const uint8_t* w2, const float* w2s, int variant,
                         hipStream_t s) {
     if (p.T <= 0) return hipSuccess;
     if (variant >= 3 && variant <= 4) return launch_gemm2_tile(p, w2, w2s, variant, s);
-    const int bm = gemm2_bm(variant);
-    dim3 grid(HB, max_mtiles(p.T, bm));
     switch (variant) {
-        case 0:
-            hipLaunchKernelGGL((gemm2_stream_kernel<1, 4>), grid, dim3(256), 0, s, p, w2, w2s);
-            break;
-        case 1:
-            hipLaunchKernelGGL((gemm2_stream_kernel<2, 4>), grid, dim3(256), 0, s, p, w2, w2s);
-            break;
-        case 2:
-            hipLaunchKernelGGL((gemm2_stream_kernel<4, 2>), grid, dim3(256), 0, s, p, w2, w2s);
-            break;
-        default:
-            hipLaunchKernelGGL((gemm2_stream_kernel<1, 8>), grid, dim3(256), 0, s, p, w2, w2s);
-            break;
+        case 0: launch_stream2<1, 4, 4, 2>(p, w2, w2s, s); break;
+        case 1: launch_stream2<2, 4, 4, 2>(p, w2, w2s, s); break;
+        case 2: launch_stream2<4, 2, 4, 2>(p, w2, w2s, s); break;
+        case 5: launch_stream2<1, 4, 1, 2>(p, w2, w2s, s); break;
+        case 6: launch_stream2<1, 4, 1, 1>(p, w2, w2s, s); break;
+        case 7: launch_stream2<2, 4, 1, 2>(p, w2, w2s, s); break;
+        case 8: launch_stream2<1, 8, 4, 2>(p, w2, w2s, s); break;
+        case 11: launch_stream2<1, 8, 1, 1>(p, w2, w2s, s); break;
+        case 12: launch_stream2<2, 4, 1, 1>(p, w2, w2s, s); break;
+        default: launch_stream2<1, 2, 1, 2>(p, w2, w2s, s); break;
     }
     return hipGetLastError();
 }

@@ -1,7 +1,7 @@
 // Grouped GEMM2 (down projection), LDS-tiled variant for many rows per expert.
 //
 // Same contract as gemm2_stream_kernel (solution/triton/kernel.py:193-293):
-//   part[s, n] = sum_kb sb2[e, n/128, kb] * (act[s, kb-block] . W2[e, n, kb-block])
+//   part[s, n] = bf16(w_s * sum_kb sb2[e, n/128, kb] * (act[s, kb-block] . W2[e, n, kb-block]))
 // with bf16 activations and fp8 weights widened to bf16 (exact).
 //
 // A workgroup of WM x WN waves computes BM = 64*WM rows x BN = 64*WN output
@@ -153,15 +153,17 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm2_tile_kernel(Plan p,
         __syncthreads();
     }
 
+    // Epilogue: routing weight (kernel.py:364) and bf16 store for the combine.
 #pragma unroll
     for (int m = 0; m < 4; ++m) {
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
             const int row = wm * 64 + m * 16 + g * 4 + i;
             if (row < nrows) {
-                float* dst = p.part + (size_t)(row0 + row) * H + n0 + wn * 64 + r;
+                const float w = p.sorted_w[row0 + row];
+                uint16_t* dst = p.part + (size_t)(row0 + row) * H + n0 + wn * 64 + r;
 #pragma unroll
-                for (int n = 0; n < 4; ++n) dst[n * 16] = acc[m][n][i];
+                for (int n = 0; n < 4; ++n) dst[n * 16] = f2bf(w * acc[m][n][i]);
             }
         }
     }

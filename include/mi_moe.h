@@ -66,7 +66,7 @@ typedef struct mi_moe_args {
  *   tok_slot   int32 [T, 8]   slots of each token, ascending local expert, -1 pad
  *   chunk_cnt  int32 [ceil(T/1024), 32]  per-1024-token-chunk local expert counts
  *   act        bf16  [8T, 2048]  SwiGLU(GEMM1) per slot
- *   part       fp32  [8T, 7168]  GEMM2 per slot (unweighted)               */
+ *   part       bf16  [8T, 7168]  routing weight x GEMM2 row per slot        */
 typedef struct mi_moe_layout {
     size_t topk_ids, topk_w, expert_off, sorted_tok, sorted_w, tok_slot, chunk_cnt, act, part;
     size_t total;

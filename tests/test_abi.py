@@ -40,7 +40,7 @@ def test_workspace_layout_monotone_and_aligned():
         assert offs == sorted(offs)
         assert all(o % 256 == 0 for o in offs)
         assert L.total == _lib.workspace_size(T) and L.total > prev
-        assert L.total - L.part >= 8 * T * 7168 * 4
+        assert L.total - L.part >= 8 * T * 7168 * 2
         prev = L.total
 
 
