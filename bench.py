@@ -20,10 +20,15 @@ other configurations; ``cpu_baseline`` the CPU oracle on this host.
 from __future__ import annotations
 
 import argparse
+import csv
+import glob
 import json
 import os
+import shutil
 import statistics
+import subprocess
 import sys
+import tempfile
 import time
 
 import torch
@@ -154,6 +159,54 @@ def time_workload(wl, steps, warmup, trials=5):
     return res
 
 
+def pmc_traffic(workload, kernel_key, copy_mib=1024, timeout=180):
+    """HBM bytes per launch of the first kernel whose name contains
+    ``kernel_key``, from two rocprofv3 counter passes (FETCH_SIZE, then
+    WRITE_SIZE) over a short child run of this bench. Each pass also times a
+    device copy of ``copy_mib`` MiB, whose counter reading gives the scale
+    from counter units to bytes. Returns None if rocprofv3 is unavailable or
+    a pass fails. Must run before this process touches the GPU."""
+    exe = shutil.which("rocprofv3")
+    if exe is None:
+        return None
+    out = {"kernel_key": kernel_key, "copy_bytes": copy_mib << 20}
+    env = dict(os.environ, TMPDIR="/tmp")
+    for counter in ("FETCH_SIZE", "WRITE_SIZE"):
+        with tempfile.TemporaryDirectory(dir="/tmp") as d:
+            cmd = ["timeout", "-s", "KILL", str(timeout), exe, "--pmc", counter, "--output-format",
+                   "csv", "-d", d, "-o", "pmc", "--", sys.executable, "-u",
+                   os.path.abspath(__file__), "--workload", workload, "--steps", "2",
+                   "--warmup", "1", "--no-sweep", "--no-cpu", "--no-pmc",
+                   "--copy-calib-mib", str(copy_mib)]
+            log(f"[bench] counter pass {counter} ...")
+            r = subprocess.run(cmd, capture_output=True, text=True, env=env, cwd="/tmp")
+            files = glob.glob(os.path.join(d, "**", "*counter_collection.csv"), recursive=True)
+            if r.returncode != 0 or not files:
+                log(f"[bench] counter pass {counter} failed (rc={r.returncode}); traffic = null")
+                return None
+            kern, copy = [], []
+            with open(files[0]) as f:
+                for row in csv.DictReader(f):
+                    if row["Counter_Name"] != counter:
+                        continue
+                    v = float(row["Counter_Value"])
+                    if kernel_key in row["Kernel_Name"]:
+                        kern.append(v)
+                    elif "copyBuffer" in row["Kernel_Name"]:
+                        copy.append(v)
+            if not kern or not copy:
+                return None
+            k_units = statistics.median(kern)
+            c_units = max(copy)  # the calibration copy is the largest copy dispatch
+            scale = (copy_mib << 20) / c_units if c_units > 0 else 0.0
+            key = "fetch" if counter == "FETCH_SIZE" else "write"
+            out[f"{key}_counter"] = k_units
+            out[f"{key}_copy_counter"] = c_units
+            out[f"{key}_bytes"] = k_units * scale
+    out["bytes"] = out["fetch_bytes"] + out["write_bytes"]
+    return out
+
+
 def cpu_baseline(wl, reps=3):
     """The CPU oracle (fp32 torch) on this host: 1 warmup + reps timed calls."""
     from oracle import ref_moe as R
@@ -181,15 +234,29 @@ def main():
     ap.add_argument("--sweep", dest="sweep", action="store_true", default=True)
     ap.add_argument("--no-sweep", dest="sweep", action="store_false")
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--no-pmc", action="store_true",
+                    help="skip the rocprofv3 FETCH_SIZE / WRITE_SIZE passes (traffic = null)")
+    ap.add_argument("--copy-calib-mib", type=int, default=0,
+                    help="(counter passes) copy this many MiB device-to-device before timing")
     a = ap.parse_args()
     if a.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU: this operator is one expert-parallel shard "
               "(local_expert_offset selects the shard) and has no multi-GPU path. "
               "Run with --gpus 1.", file=sys.stderr)
         sys.exit(2)
+    traffic = None
+    if not a.no_pmc:
+        # counter passes run as child processes before this one uses the GPU
+        traffic = pmc_traffic(a.workload, "gemm1_")
     if not torch.cuda.is_available():
         print("bench.py needs a ROCm GPU", file=sys.stderr)
         sys.exit(2)
+    if a.copy_calib_mib > 0:
+        src = torch.empty(a.copy_calib_mib << 20, dtype=torch.uint8, device="cuda")
+        dst = torch.empty_like(src)
+        dst.copy_(src)
+        torch.cuda.synchronize()
+        del src, dst
     from flashinfer_amd import _lib
     _lib.lib()
 
@@ -233,11 +300,13 @@ def main():
                    "parallelism": "single GPU (one EP shard)"},
         "roofline": {"kernel": "gemm1_swiglu", "bound": "hbm", "achieved": round(achieved, 1),
                      "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
+                     "frac": round(achieved / HBM_PEAK_GBS, 4),
+                     "traffic": round(traffic["bytes"]) if traffic else None,
                      "algorithmic_bytes_per_launch": g1_bytes, "avg_launch_us": round(g1_us, 2)},
         "call_roofline": {"gbps": head["gbps"], "hbm_frac": head["hbm_frac"],
                           "tflops": head["tflops"], "roofline_frac": head["roofline_frac"],
                           "phase_us": head["phase_us"]},
+        "traffic_detail": traffic,
         "cpu_baseline": cpu,
         "sweep": sweep,
     }
