@@ -11,7 +11,9 @@ bound by HBM bandwidth. W untimed calls, then 5 trials of K calls each,
 bracketed by ``torch.cuda.synchronize()``; ``value`` is the median trial's
 microseconds per call. A second pass of 5 x K calls records HIP events
 between the five kernels on the stream they run on, which gives each
-kernel's average duration.
+kernel's average duration. A third pass times single calls with the caches
+cold (a 512 MiB read before each call evicts the MALL and L2s), and the
+probes of libmi_peaks.so measure the HBM and MFMA rates this GPU achieves.
 
 Rank 0 prints ONE JSON line. ``roofline`` covers the dominant kernel
 (GEMM1+SwiGLU at decode); ``call_roofline`` the whole call; ``sweep`` the
@@ -44,7 +46,7 @@ W1_EXPERT_BYTES = 2 * I * H + (2 * I // BLOCK) * (H // BLOCK) * 4        # 29,36
 W2_EXPERT_BYTES = H * I + (H // BLOCK) * (I // BLOCK) * 4                # 14,683,648
 HS_ROW_BYTES = H + (H // BLOCK) * 4                                      # fp8 row + scales
 ACT_ROW_BYTES = I * 2                                                    # bf16 SwiGLU row
-PART_ROW_BYTES = H * 4                                                   # fp32 GEMM2 row
+PART_ROW_BYTES = H * 2                                                   # bf16 weighted GEMM2 row
 GEMM1_FLOPS_PER_SLOT = 2 * 2 * I * H
 GEMM2_FLOPS_PER_SLOT = 2 * H * I
 
@@ -131,12 +133,16 @@ def time_workload(wl, steps, warmup, trials=5):
             for p in range(_lib.NUM_PHASES):
                 phase_sum[p] += ev[k][p].elapsed_time(ev[k][p + 1]) * 1e3
     phase_us = [s / (steps * trials) for s in phase_sum]
+    cold_us = time_cold(args, out, min(steps, 20))
     us = statistics.median(trial_us)
     B = call_bytes(wl.T, A_e)
     F1, F2 = S * GEMM1_FLOPS_PER_SLOT, S * GEMM2_FLOPS_PER_SLOT
     F = F1 + F2
     t = us * 1e-6
     bound_t = max(B / (HBM_PEAK_GBS * 1e9), F / (FP8_PEAK_TFLOPS * 1e12))
+    # GEMM2 runs on bf16 MFMA: the bound with its flops priced at the bf16 peak
+    mixed_t = max(B / (HBM_PEAK_GBS * 1e9),
+                  F1 / (FP8_PEAK_TFLOPS * 1e12) + F2 / (BF16_PEAK_TFLOPS * 1e12))
     res = {
         "workload": wl.name, "T": wl.T, "local_expert_offset": wl.local_expert_offset,
         "slots": S, "active_experts": A_e, "max_rows_per_expert": max_rows,
@@ -146,6 +152,8 @@ def time_workload(wl, steps, warmup, trials=5):
         "hbm_frac": round(B / t / 1e9 / HBM_PEAK_GBS, 4),
         "fp8_frac": round(F / t / 1e12 / FP8_PEAK_TFLOPS, 4),
         "roofline_frac": round(bound_t / t, 4),
+        "mixed_roofline_frac": round(mixed_t / t, 4),
+        "us_per_call_cold": round(cold_us, 2),
         "algorithmic_bytes": B, "algorithmic_flops": F,
         "phase_us": {n: round(v, 2) for n, v in zip(_lib.PHASES, phase_us)},
     }
@@ -157,6 +165,86 @@ def time_workload(wl, steps, warmup, trials=5):
     res["gemm2_tflops"] = round(F2 / g2 / 1e12, 2) if g2 > 0 else None
     del args, out
     return res
+
+
+def time_cold(args, out, steps, flush_mib=512):
+    """Median microseconds of one call with the caches cold: before each call
+    a 512 MiB read evicts the 256 MB MALL and the L2s (a read, so no dirty
+    lines are written back during the call); HIP events on the call's stream
+    bracket the call alone."""
+    from flashinfer_amd import kernel
+    flush = torch.ones((flush_mib << 20) // 4, dtype=torch.float32, device=out.device)
+    sink = torch.empty((), dtype=torch.float32, device=out.device)
+    ts = []
+    for _ in range(steps):
+        torch.sum(flush, dim=0, out=sink)
+        e0 = torch.cuda.Event(enable_timing=True)
+        e1 = torch.cuda.Event(enable_timing=True)
+        e0.record()
+        kernel.run(*args, out)
+        e1.record()
+        e1.synchronize()
+        ts.append(e0.elapsed_time(e1) * 1e3)
+    del flush
+    return statistics.median(ts)
+
+
+def measured_peaks():
+    """Achievable rates on this GPU, from the probes in libmi_peaks.so
+    (include/mi_peaks.h): an HBM read and copy (best workgroup count of a
+    small sweep, median of 5 launches each) and dense fp8 / bf16 MFMA loops."""
+    import ctypes
+    path = os.path.join(os.path.dirname(os.path.abspath(__file__)), "flashinfer_amd",
+                        "libmi_peaks.so")
+    if not os.path.exists(path):
+        log("[bench] libmi_peaks.so missing; measured peaks skipped")
+        return None
+    L = ctypes.CDLL(path)
+    vp, i32, i64, sz = ctypes.c_void_p, ctypes.c_int32, ctypes.c_int64, ctypes.c_size_t
+    L.mi_peak_read.argtypes = [vp, sz, i32, vp, vp]
+    L.mi_peak_copy.argtypes = [vp, vp, sz, i32, vp]
+    L.mi_peak_mfma.argtypes = [i32, i64, i32, vp, vp]
+    L.mi_peak_mfma_flops.argtypes = [i32, i64, i32]
+    L.mi_peak_mfma_flops.restype = ctypes.c_double
+    stream = vp(torch.cuda.current_stream().cuda_stream)
+
+    def best(launch, reps=5):
+        launch()
+        ts = []
+        for _ in range(reps):
+            e0 = torch.cuda.Event(enable_timing=True)
+            e1 = torch.cuda.Event(enable_timing=True)
+            e0.record()
+            rc = launch()
+            e1.record()
+            e1.synchronize()
+            if rc != 0:
+                raise RuntimeError(f"peak probe returned {rc}")
+            ts.append(e0.elapsed_time(e1) * 1e-3)
+        return statistics.median(ts)
+
+    nbytes = 2 << 30
+    a = torch.ones(nbytes, dtype=torch.uint8, device="cuda")
+    b = torch.empty_like(a)
+    sink = torch.zeros(8192 * 256, dtype=torch.float32, device="cuda")
+    wgs = (512, 1024, 2048, 4096)
+    read = max(nbytes / best(lambda: L.mi_peak_read(a.data_ptr(), nbytes, wg, sink.data_ptr(), stream))
+               for wg in wgs)
+    half = nbytes // 2
+    copy = max(2 * half / best(lambda: L.mi_peak_copy(b.data_ptr(), a.data_ptr(), half, wg, stream))
+               for wg in wgs)
+    del a, b
+    out = {"hbm_read_gbs": round(read / 1e9, 1), "hbm_copy_gbs": round(copy / 1e9, 1),
+           "copy_counts": "read + write bytes"}
+    for kind, key in ((0, "fp8_mfma_tflops"), (1, "bf16_mfma_tflops")):
+        rates = []
+        for wg in (512, 1024):
+            iters = 4000 if kind == 0 else 8000
+            t = best(lambda: L.mi_peak_mfma(kind, iters, wg, sink.data_ptr(), stream), reps=3)
+            rates.append(L.mi_peak_mfma_flops(kind, iters, wg) / t)
+        out[key] = round(max(rates) / 1e12, 1)
+    del sink
+    return out
 
 
 def pmc_traffic(workload, kernel_key, copy_mib=1024, timeout=180):
@@ -219,10 +307,19 @@ def cpu_baseline(wl, reps=3):
         t0 = time.perf_counter()
         R.moe_forward(*args)
         ts.append(time.perf_counter() - t0)
+    # A definition-style reference dequantises every local expert's weights
+    # each call; timed separately (one pass over the 32 experts).
+    t = wl.tensors
+    t0 = time.perf_counter()
+    for e in range(t["gemm1_weights"].shape[0]):
+        R.dequant_blocks(t["gemm1_weights"][e], t["gemm1_weights_scale"][e])
+        R.dequant_blocks(t["gemm2_weights"][e], t["gemm2_weights_scale"][e])
+    dq_all = time.perf_counter() - t0
     return {"value": round(statistics.median(ts) * 1e6, 1), "unit": "us/call", "cores": cores,
             "kind": "port",
             "sample": f"full {wl.name} call (T={wl.T}), fp32 torch oracle, dequantising only the "
-                      f"active experts, 1 warmup + {reps} timed, median"}
+                      f"active experts, 1 warmup + {reps} timed, median",
+            "dequant_all_experts_us": round(dq_all * 1e6, 1)}
 
 
 def main():
@@ -278,6 +375,11 @@ def main():
             log(f"[bench] {json.dumps(r)}")
             sweep.append(r)
             del w
+    peaks = None
+    if a.copy_calib_mib == 0:  # not in the counter passes: their largest copy calibrates
+        peaks = measured_peaks()
+        log(f"[bench] measured peaks {peaks}")
+    read_gbs = peaks["hbm_read_gbs"] if peaks else None
     cpu = None
     if not a.no_cpu:
         log("[bench] CPU oracle baseline ...")
@@ -293,7 +395,7 @@ def main():
         "warmup": a.warmup, "ms_per_step": round(head["us_per_call"] / 1000.0, 5),
         "higher_is_better": False, "scaling": "weak", "vs_baseline": None, "dtype": "fp8_e4m3 (GEMM1) / bf16 (GEMM2), fp32 accumulate",
         "data": "synthetic (seeded N(0,1) fp8 weights/activations, U scales, N(0,0.1) bias)",
-        "config": {"workload": f"decode sweep T={wl.T} (configs[1])", "T": wl.T,
+        "config": {"workload": f"{wl.name}: one fused-MoE layer call, T={wl.T} tokens", "T": wl.T,
                    "H": H, "I": I, "experts_global": E_GLOBAL, "experts_local": 32, "top_k": 8,
                    "local_expert_offset": wl.local_expert_offset,
                    "slots": head["slots"], "active_experts": head["active_experts"],
@@ -302,9 +404,14 @@ def main():
                      "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(achieved / HBM_PEAK_GBS, 4),
                      "traffic": round(traffic["bytes"]) if traffic else None,
-                     "algorithmic_bytes_per_launch": g1_bytes, "avg_launch_us": round(g1_us, 2)},
+                     "algorithmic_bytes_per_launch": g1_bytes, "avg_launch_us": round(g1_us, 2),
+                     "measured_read_gbs": read_gbs,
+                     "frac_of_measured_read": round(achieved / read_gbs, 4) if read_gbs else None},
+        "measured_peaks": peaks,
         "call_roofline": {"gbps": head["gbps"], "hbm_frac": head["hbm_frac"],
                           "tflops": head["tflops"], "roofline_frac": head["roofline_frac"],
+                          "mixed_roofline_frac": head["mixed_roofline_frac"],
+                          "us_per_call_cold": head["us_per_call_cold"],
                           "phase_us": head["phase_us"]},
         "traffic_detail": traffic,
         "cpu_baseline": cpu,

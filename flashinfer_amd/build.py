@@ -1,7 +1,8 @@
-"""Builds libmi_moe.so (all HIP kernels + the C ABI) for gfx950 with hipcc.
+"""Builds libmi_moe.so (all HIP kernels + the C ABI) and libmi_peaks.so
+(achievable-peak probes used by bench.py) for gfx950 with hipcc.
 
 Usage: python -m flashinfer_amd.build [--jobs N] [--save-temps]
-The shared library lands next to this file so it travels with the tree.
+The shared libraries land next to this file so they travel with the tree.
 """
 from __future__ import annotations
 
@@ -18,6 +19,16 @@ BUILD = os.path.join(HERE, "_build")
 LIB = os.path.join(HERE, "libmi_moe.so")
 SOURCES = ["route.hip", "sort.hip", "gemm1.hip", "gemm2.hip", "gemm1_tile.hip", "gemm2_tile.hip",
            "gemm2_combine.hip", "combine.hip", "capi.hip"]
+PEAKS_LIB = os.path.join(HERE, "libmi_peaks.so")
+PEAKS_SOURCES = ["peaks.hip"]
+# Per-source flags: MFMA results in VGPRs rather than AGPRs.
+# * peaks.hip: in the default AGPR form the compiler gives the bf16 MFMA
+#   loop partially overlapping srcC / vdst registers and shuffles every
+#   chain through VGPRs each round.
+# * gemm1.hip: each MFMA result is scaled in VALU; the VGPR form drops a
+#   v_accvgpr_read per result register (GEMM1 stream 1% faster at T=64).
+SOURCE_FLAGS = {"peaks.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"],
+                "gemm1.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"]}
 ARCH = "gfx950"
 
 HIPCC_FLAGS = [
@@ -40,7 +51,8 @@ def hipcc() -> str:
 
 def _compile(src: str, extra) -> str:
     obj = os.path.join(BUILD, src.replace(".hip", ".o"))
-    cmd = [hipcc(), *HIPCC_FLAGS, *extra, "-I", os.path.join(HERE, "..", "include"),
+    cmd = [hipcc(), *HIPCC_FLAGS, *SOURCE_FLAGS.get(src, []), *extra,
+           "-I", os.path.join(HERE, "..", "include"),
            "-c", os.path.join(CSRC, src), "-o", obj]
     r = subprocess.run(cmd, capture_output=True, text=True)
     if r.returncode != 0:
@@ -51,17 +63,22 @@ def _compile(src: str, extra) -> str:
     return obj
 
 
-def build(jobs: int = 8, extra=()) -> str:
-    os.makedirs(BUILD, exist_ok=True)
-    with ThreadPoolExecutor(max_workers=jobs) as ex:
-        objs = list(ex.map(lambda s: _compile(s, list(extra)), SOURCES))
-    tmp = LIB + ".tmp"
+def _link(objs, out):
+    tmp = out + ".tmp"
     cmd = [hipcc(), f"--offload-arch={ARCH}", "-mcode-object-version=5", "-shared", "-fPIC",
            *objs, "-o", tmp]
     r = subprocess.run(cmd, capture_output=True, text=True)
     if r.returncode != 0:
-        raise RuntimeError(f"link failed:\n{r.stderr}")
-    os.replace(tmp, LIB)
+        raise RuntimeError(f"link of {os.path.basename(out)} failed:\n{r.stderr}")
+    os.replace(tmp, out)
+
+
+def build(jobs: int = 8, extra=()) -> str:
+    os.makedirs(BUILD, exist_ok=True)
+    with ThreadPoolExecutor(max_workers=jobs) as ex:
+        objs = list(ex.map(lambda s: _compile(s, list(extra)), SOURCES + PEAKS_SOURCES))
+    _link(objs[:len(SOURCES)], LIB)
+    _link(objs[len(SOURCES):], PEAKS_LIB)
     return LIB
 
 

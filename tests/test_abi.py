@@ -12,10 +12,10 @@ from flashinfer_amd import _lib, kernel
 ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 
 
-def _declared_functions():
-    src = open(os.path.join(ROOT, "include", "mi_moe.h")).read()
+def _declared_functions(header="mi_moe.h", prefix="mi_moe_"):
+    src = open(os.path.join(ROOT, "include", header)).read()
     src = re.sub(r"/\*.*?\*/", "", src, flags=re.S)
-    return sorted(set(re.findall(r"\b(mi_moe_[a-z_]+)\s*\(", src)))
+    return sorted(set(re.findall(r"\b(" + prefix + r"[a-z0-9_]+)\s*\(", src)))
 
 
 def test_library_exports_every_declared_symbol():
@@ -25,6 +25,25 @@ def test_library_exports_every_declared_symbol():
     for name in decl:
         assert hasattr(L, name), f"{name} declared in mi_moe.h but not exported"
     assert set(decl) == set(_lib.EXPORTED)
+
+
+def test_peaks_library_exports_every_declared_symbol():
+    L = ctypes.CDLL(os.path.join(ROOT, "flashinfer_amd", "libmi_peaks.so"))
+    decl = _declared_functions("mi_peaks.h", "mi_peak_")
+    assert decl == ["mi_peak_copy", "mi_peak_mfma", "mi_peak_mfma_flops", "mi_peak_read"]
+    for name in decl:
+        assert hasattr(L, name), f"{name} declared in mi_peaks.h but not exported"
+    # argument checks return before any launch
+    L.mi_peak_read.argtypes = [ctypes.c_void_p, ctypes.c_size_t, ctypes.c_int32, ctypes.c_void_p,
+                               ctypes.c_void_p]
+    assert L.mi_peak_read(None, 16, 1024, None, None) == 1
+    assert L.mi_peak_read(1 << 20, 15, 1024, 1 << 21, None) == 1
+    L.mi_peak_mfma.argtypes = [ctypes.c_int32, ctypes.c_int64, ctypes.c_int32, ctypes.c_void_p,
+                               ctypes.c_void_p]
+    assert L.mi_peak_mfma(2, 10, 512, 1 << 20, None) == 1
+    L.mi_peak_mfma_flops.argtypes = [ctypes.c_int32, ctypes.c_int64, ctypes.c_int32]
+    L.mi_peak_mfma_flops.restype = ctypes.c_double
+    assert L.mi_peak_mfma_flops(0, 10, 512) == 2 * 16 * 16 * 128 * 8 * 4 * 512 * 10
 
 
 def test_version():
