@@ -146,10 +146,10 @@ hipError_t launch_gemm2_tile(const Plan& p, const uint8_t* w2, const float* w2s,
 
 // GEMM kernel variants: 0/1/2 weight-streaming with 16/32/64-row tiles and
 // 4-wave workgroups, 3 LDS-tiled large (GEMM1 256 rows, GEMM2 128 rows),
-// 4 LDS-tiled medium (GEMM1 128 rows, GEMM2 64 rows), 5..12 weight-streaming
-// shapes with 1- or 2-wave workgroups (see the launchers), 10 GEMM2 fused
-// with the combine.
-constexpr int NUM_VARIANTS = 13;
+// 4 LDS-tiled medium (GEMM1 128 rows, GEMM2 64 rows), 5..14 weight-streaming
+// shapes with 1-, 2-, 4- or 8-wave workgroups and 16/32/64 columns per wave
+// (see the launchers), 10 GEMM2 fused with the combine.
+constexpr int NUM_VARIANTS = 15;
 // GEMM2 variant that also performs the combine (decode sizes only).
 constexpr int VARIANT_GEMM2_COMBINE = 10;
 

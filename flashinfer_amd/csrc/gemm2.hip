@@ -90,7 +90,7 @@ __global__ __launch_bounds__(64 * NW) void gemm2_stream_kernel(Plan p, const uin
 #pragma unroll
         for (int i = 0; i < MT; ++i) {
 #pragma unroll
-            for (int q = 0; q < 2; ++q) {
+            for (int q = 0; q < NQ; ++q) {
                 const v4f pr = mfma_block(a[d][i], b[d][q]);
                 acc[i][q][0] += pr[0] * sb;
                 acc[i][q][1] += pr[1] * sb;
@@ -169,6 +169,8 @@ hipError_t launch_gemm2(const Plan& p, const uint8_t* w2, const float* w2s, int 
         case 8: launch_stream2<1, 8, 4, 2>(p, w2, w2s, s); break;
         case 11: launch_stream2<1, 8, 1, 1>(p, w2, w2s, s); break;
         case 12: launch_stream2<2, 4, 1, 1>(p, w2, w2s, s); break;
+        case 13: launch_stream2<1, 4, 1, 4>(p, w2, w2s, s); break;
+        case 14: launch_stream2<1, 2, 1, 4>(p, w2, w2s, s); break;
         default: launch_stream2<1, 2, 1, 2>(p, w2, w2s, s); break;
     }
     return hipGetLastError();
