@@ -73,8 +73,12 @@ bool fuse_front_end(int64_t T) {
 
 Variants pick_variants(int64_t T) {
     Variants v;
-    if (T <= 128) v = {5, 5};
-    else if (T <= 256) v = {1, 1};
+    // Measured on MI355X: single-wave streaming workgroups while an expert
+    // has at most a few row tiles, 64-column GEMM2 waves from T = 64, the
+    // LDS-tiled kernels once experts hold hundreds of rows.
+    if (T <= 32) v = {5, 5};
+    else if (T <= 128) v = {5, 14};
+    else if (T <= 256) v = {1, 13};
     else v = {3, 3};
     const char* env = getenv("MI_MOE_VARIANT");
     if (env && *env) {

@@ -31,13 +31,12 @@ struct G1Tile {
     static constexpr int B_BYTES = 2 * BG * BLK;
     static constexpr int SA_BYTES = BM * 4;
     static constexpr int STAGE = A_BYTES + B_BYTES + SA_BYTES;
-    static constexpr int SCRATCH = 256 * NW;  // L2-prefetch landing area
     static constexpr int A_LD = A_BYTES / 1024 / NW;  // 1 KB copies per wave per stage
     static constexpr int B_LD = B_BYTES / 1024 / NW;
     static constexpr int SA_WAVES = BM / 64;          // waves copying one scale each per lane
     static_assert(A_BYTES % (1024 * NW) == 0 && B_BYTES % (1024 * NW) == 0, "loader split");
     static_assert(SA_WAVES <= NW, "scale loader");
-    static_assert(2 * STAGE + SCRATCH <= 160 * 1024, "LDS budget");
+    static_assert(2 * STAGE <= 160 * 1024, "LDS budget");
 };
 
 template <int WM, int WN, int GM>
@@ -45,7 +44,7 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm1_tile_kernel(
     Plan p, const uint8_t* __restrict__ hs, const float* __restrict__ hs_scale,
     const uint8_t* __restrict__ w1, const float* __restrict__ w1s) {
     using C = G1Tile<WM, WN>;
-    __shared__ __attribute__((aligned(1024))) uint8_t smem[2 * C::STAGE + C::SCRATCH];
+    __shared__ __attribute__((aligned(1024))) uint8_t smem[2 * C::STAGE];
 
     int e, row0, nrows, nt;
     if (!tile_coords<C::NT, GM>(p.meta, META_MTILE1, C::BM, e, row0, nrows, nt)) return;
@@ -71,16 +70,6 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm1_tile_kernel(
         const int c = (lane & 7) ^ swz8(row);
         const int wrow = row < C::BG ? jb + row : I + jb + (row - C::BG);
         b_off[i] = (uint32_t)((e * N1 + wrow) * H + c * 16);
-    }
-    // L2 prefetch of k-block kb+2: lanes 0..31 touch the wave's A rows, lanes
-    // 32..63 its B rows (one 128-byte line each).
-    const uint8_t* pf_base;
-    {
-        const int prow = C::BM / C::NW * wave + (lane & 31) % (C::BM / C::NW);
-        const int brow = (2 * C::BG) / C::NW * wave + (lane & 31) % ((2 * C::BG) / C::NW);
-        const int tok = p.sorted_tok[row0 + min(prow, nrows - 1)];
-        const int wrow = brow < C::BG ? jb + brow : I + jb + (brow - C::BG);
-        pf_base = lane < 32 ? hs + (size_t)tok * H : w1 + ((size_t)e * N1 + wrow) * H;
     }
     uint32_t sa_off = 0;
     if (wave < C::SA_WAVES) {
@@ -116,27 +105,35 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm1_tile_kernel(
     wait_vmem();
     __syncthreads();
 
-    uint8_t* pf_lds = smem + 2 * C::STAGE + 256 * wave;
-    prefetch_l2(pf_base + 1 * BLK, pf_lds);
-
 #pragma unroll 1
     for (int kb = 0; kb < HB; ++kb) {
         const int cur = kb & 1;
-        if (kb + 1 < HB) issue(cur ^ 1, kb + 1);
-        prefetch_l2(pf_base + min(kb + 2, HB - 1) * BLK, pf_lds);
         const uint8_t* sA = smem + cur * C::STAGE;
         const uint8_t* sB = sA + C::A_BYTES;
         const float* sSA = reinterpret_cast<const float*>(sB + C::B_BYTES);
 
+        // Waves whose 64 rows lie past the expert's last row (partial row
+        // tiles) only copy; the branch is wave-uniform.
+        const bool active = wm * 64 < nrows;
         v8i a[4];
+        if (active) {
 #pragma unroll
-        for (int m = 0; m < 4; ++m) {
-            const int row = wm * 64 + m * 16 + r;
-            const uint8_t* base = sA + row * BLK;
-            const int sw = swz8(row);
-            const v4i lo = lds16(base + ((g ^ sw) << 4));
-            const v4i hi = lds16(base + (((g + 4) ^ sw) << 4));
-            a[m] = (v8i){lo.x, lo.y, lo.z, lo.w, hi.x, hi.y, hi.z, hi.w};
+            for (int m = 0; m < 4; ++m) {
+                const int row = wm * 64 + m * 16 + r;
+                const uint8_t* base = sA + row * BLK;
+                const int sw = swz8(row);
+                const v4i lo = lds16(base + ((g ^ sw) << 4));
+                const v4i hi = lds16(base + (((g + 4) ^ sw) << 4));
+                a[m] = (v8i){lo.x, lo.y, lo.z, lo.w, hi.x, hi.y, hi.z, hi.w};
+            }
+        }
+        // The copy of k-block kb+1 goes out after this wave's A reads, so its
+        // LDS writes do not compete with them.
+        if (kb + 1 < HB) issue(cur ^ 1, kb + 1);
+        if (!active) {
+            wait_vmem();
+            __syncthreads();
+            continue;
         }
         // Per-row scale products sa*sb for the gate half, then (re-read from
         // LDS) for the up half: one set of 16 registers instead of two.
@@ -177,10 +174,9 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm1_tile_kernel(
                 acc[m][n][3] += pr[m][3] * cs[m][3];
             }
         }
-        wait_vmem_but_one();
+        wait_vmem();
         __syncthreads();
     }
-    wait_vmem();
 
 #pragma unroll
     for (int m = 0; m < 4; ++m) {

@@ -37,19 +37,6 @@ __device__ __forceinline__ void g2l4(const void* gsrc, void* lds_base) {
 
 __device__ __forceinline__ void wait_vmem() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
 
-// Waits for all but the most recent vector-memory load (loads return in
-// order), leaving one L2 prefetch in flight.
-__device__ __forceinline__ void wait_vmem_but_one() {
-    asm volatile("s_waitcnt vmcnt(1)" ::: "memory");
-}
-
-// L2 prefetch: a 4-byte LDS-DMA load of one cache line per lane into a
-// per-wave scratch area of 256 bytes in LDS (no VGPR is written), so that a
-// later copy of the line hits L2. Issue it after the copies it must not delay.
-__device__ __forceinline__ void prefetch_l2(const void* gsrc, void* lds_scratch) {
-    g2l4(gsrc, lds_scratch);
-}
-
 // XOR swizzle of the 16-byte chunk index inside a 128-byte LDS row: 16
 // consecutive rows reading the same logical chunk hit 16 distinct 16-byte
 // bank groups (conflict-free for 32- and 64-bank LDS).
