@@ -17,7 +17,8 @@ probes of libmi_peaks.so measure the HBM and MFMA rates this GPU achieves.
 
 Rank 0 prints ONE JSON line. ``roofline`` covers the dominant kernel
 (GEMM1+SwiGLU at decode); ``call_roofline`` the whole call; ``sweep`` the
-other configurations; ``cpu_baseline`` the CPU oracle on this host.
+other configurations; ``quantize_fp8`` the activation quantiser that
+feeds the operator; ``cpu_baseline`` the CPU oracle on this host.
 """
 from __future__ import annotations
 
@@ -187,6 +188,32 @@ def time_cold(args, out, steps, flush_mib=512):
         ts.append(e0.elapsed_time(e1) * 1e3)
     del flush
     return statistics.median(ts)
+
+
+def time_quantizer(T, reps=50):
+    """The FP8 activation quantiser on bf16 [T, 7168]: median µs per call and
+    HBM rate (2 B read + 1 B written per element, plus the [56, T] scales)."""
+    from flashinfer_amd import kernel
+    g = torch.Generator(device="cuda").manual_seed(T)
+    x = torch.randn(T, H, device="cuda", generator=g).to(torch.bfloat16)
+    q = torch.empty(T, H, dtype=torch.float8_e4m3fn, device="cuda")
+    s = torch.empty(H // BLOCK, T, dtype=torch.float32, device="cuda")
+    kernel.quantize_activations(x, q, s)
+    ts = []
+    for _ in range(5):
+        e0 = torch.cuda.Event(enable_timing=True)
+        e1 = torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(reps):
+            kernel.quantize_activations(x, q, s)
+        e1.record()
+        e1.synchronize()
+        ts.append(e0.elapsed_time(e1) * 1e3 / reps)
+    us = statistics.median(ts)
+    nbytes = T * H * 3 + T * (H // BLOCK) * 4
+    return {"T": T, "us_per_call": round(us, 2), "bytes": nbytes,
+            "gbps": round(nbytes / (us * 1e-6) / 1e9, 1),
+            "hbm_frac": round(nbytes / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4)}
 
 
 def measured_peaks():
@@ -375,6 +402,9 @@ def main():
             log(f"[bench] {json.dumps(r)}")
             sweep.append(r)
             del w
+    quant = [time_quantizer(T) for T in (64, 8192)] if a.sweep else []
+    for qr in quant:
+        log(f"[bench] quantiser {qr}")
     peaks = None
     if a.copy_calib_mib == 0:  # not in the counter passes: their largest copy calibrates
         peaks = measured_peaks()
@@ -416,6 +446,7 @@ def main():
         "traffic_detail": traffic,
         "cpu_baseline": cpu,
         "sweep": sweep,
+        "quantize_fp8": quant,
     }
     print(json.dumps(line), flush=True)
 

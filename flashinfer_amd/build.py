@@ -18,7 +18,7 @@ CSRC = os.path.join(HERE, "csrc")
 BUILD = os.path.join(HERE, "_build")
 LIB = os.path.join(HERE, "libmi_moe.so")
 SOURCES = ["route.hip", "sort.hip", "gemm1.hip", "gemm2.hip", "gemm1_tile.hip", "gemm2_tile.hip",
-           "gemm2_combine.hip", "combine.hip", "capi.hip"]
+           "gemm2_combine.hip", "combine.hip", "quant.hip", "capi.hip"]
 PEAKS_LIB = os.path.join(HERE, "libmi_peaks.so")
 PEAKS_SOURCES = ["peaks.hip"]
 # Per-source flags: MFMA results in VGPRs rather than AGPRs.

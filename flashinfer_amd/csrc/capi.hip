@@ -135,6 +135,25 @@ int mi_moe_route(const float* routing_logits, const void* routing_bias, int32_t 
     return MI_MOE_OK;
 }
 
+int mi_moe_quantize_fp8(const void* hidden_bf16, int64_t num_tokens, uint8_t* hidden_states,
+                        float* hidden_states_scale, void* stream) {
+    g_last_error.clear();
+    if (num_tokens < 0 || num_tokens > kMaxTokens)
+        return fail(MI_MOE_ERR_INVALID, "mi_moe_quantize_fp8: num_tokens %lld out of range",
+                    (long long)num_tokens);
+    if (num_tokens == 0) return MI_MOE_OK;
+    if (!hidden_bf16 || !hidden_states || !hidden_states_scale)
+        return fail(MI_MOE_ERR_INVALID, "mi_moe_quantize_fp8: NULL pointer argument");
+    if (!aligned(hidden_bf16, 16) || !aligned(hidden_states, 16) || !aligned(hidden_states_scale, 4))
+        return fail(MI_MOE_ERR_INVALID, "mi_moe_quantize_fp8: misaligned pointer");
+    hipError_t err = launch_quant_fp8(hidden_bf16, (int)num_tokens, hidden_states,
+                                      hidden_states_scale, (hipStream_t)stream);
+    if (err != hipSuccess)
+        return fail(MI_MOE_ERR_HIP, "mi_moe_quantize_fp8: launch failed: %s",
+                    hipGetErrorString(err));
+    return MI_MOE_OK;
+}
+
 static int run_impl(const mi_moe_args* a, hipStream_t s, hipEvent_t const* ev) {
     g_last_error.clear();
     if (!a) return fail(MI_MOE_ERR_INVALID, "mi_moe_run: args is NULL");

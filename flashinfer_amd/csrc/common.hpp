@@ -136,6 +136,7 @@ hipError_t launch_gemm1(const Plan& p, const uint8_t* hs, const float* hs_scale,
 hipError_t launch_gemm2(const Plan& p, const uint8_t* w2, const float* w2s, int variant,
                         hipStream_t s);
 hipError_t launch_combine(const Plan& p, uint16_t* out, hipStream_t s);
+hipError_t launch_quant_fp8(const void* x, int T, uint8_t* q, float* scale, hipStream_t s);
 bool gemm2_combine_supported(int T);
 hipError_t launch_gemm2_combine(const Plan& p, const uint8_t* w2, const float* w2s, uint16_t* out,
                                 hipStream_t s);

@@ -202,7 +202,7 @@ hipError_t launch_gemm1_tile(const Plan& p, const uint8_t* hs, const float* hs_s
         using C = G1Tile<4, 2>;
         const int tiles = max_mtiles(p.T, C::BM) * C::NT;
         dim3 grid((tiles + 7) / 8 * 8);
-        hipLaunchKernelGGL((gemm1_tile_kernel<4, 2, 4>), grid, dim3(C::THREADS), 0, s, p, hs,
+        hipLaunchKernelGGL((gemm1_tile_kernel<4, 2, 16>), grid, dim3(C::THREADS), 0, s, p, hs,
                            hs_scale, w1, w1s);
     } else {
         using C = G1Tile<2, 2>;

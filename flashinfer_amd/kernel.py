@@ -171,6 +171,41 @@ def route(routing_logits: torch.Tensor, routing_bias: torch.Tensor, routed_scali
     return ids, w
 
 
+def quantize_activations(hidden: torch.Tensor, hidden_states: torch.Tensor | None = None,
+                         hidden_states_scale: torch.Tensor | None = None):
+    """FP8 activation quantiser feeding ``run``: bf16 ``hidden`` [T, 7168] ->
+    (``hidden_states`` fp8 e4m3fn [T, 7168], ``hidden_states_scale`` fp32
+    [56, T]), the input pair of kernel.py:600-613 in its block-major scale
+    layout (kernel.py:169). Per token and 128-element block:
+    s = max(amax, 1e-10) / 448, q = e4m3(clamp(x / s, -448, 448)), round to
+    nearest even. Inputs must be finite. Outputs may be passed in."""
+    T = int(hidden.shape[0]) if isinstance(hidden, torch.Tensor) and hidden.dim() == 2 else -1
+    _expect(hidden, "hidden", (torch.bfloat16,), (T, H))
+    dev = hidden.device
+    if hidden_states is None:
+        hidden_states = torch.empty(T, H, dtype=FP8, device=dev)
+    if hidden_states_scale is None:
+        hidden_states_scale = torch.empty(H // BLOCK, T, dtype=torch.float32, device=dev)
+    _expect(hidden_states, "hidden_states", (FP8,), (T, H))
+    _expect(hidden_states_scale, "hidden_states_scale", (torch.float32,), (H // BLOCK, T))
+    if dev.type != "cuda":
+        raise ValueError("quantize_activations runs on a ROCm GPU; got tensors on " + str(dev))
+    for t, n in ((hidden_states, "hidden_states"), (hidden_states_scale, "hidden_states_scale")):
+        if t.device != dev:
+            raise ValueError(f"{n} is on {t.device}, hidden on {dev}")
+        if not t.is_contiguous():
+            raise ValueError(f"{n} must be contiguous (it is written in place)")
+    if T == 0:
+        return hidden_states, hidden_states_scale
+    x = hidden.contiguous()
+    with torch.cuda.device(dev):
+        stream = torch.cuda.current_stream(dev).cuda_stream
+        _lib.check(_lib.lib().mi_moe_quantize_fp8(
+            x.data_ptr(), T, hidden_states.data_ptr(), hidden_states_scale.data_ptr(),
+            ctypes.c_void_p(stream)))
+    return hidden_states, hidden_states_scale
+
+
 def last_workspace(device: torch.device | None = None) -> torch.Tensor:
     """The cached workspace of the current stream (for staged parity checks)."""
     device = device or torch.device("cuda", torch.cuda.current_device())

@@ -99,6 +99,17 @@ int mi_moe_route(const float* routing_logits, const void* routing_bias, int32_t 
                  int64_t num_tokens, float routed_scaling_factor, int32_t* topk_ids,
                  float* topk_weights, void* stream);
 
+/* FP8 activation quantiser feeding mi_moe_run: bf16 hidden states [T, 7168]
+ * -> hidden_states fp8 e4m3fn [T, 7168] and hidden_states_scale fp32 [56, T]
+ * (block-major, the layout kernel.py:169 reads). Per token and 128-element
+ * block: s = max(amax, 1e-10) / 448, q = e4m3(clamp(x / s, -448, 448)),
+ * round to nearest even, IEEE fp32 division. Inputs must be finite.
+ * No counterpart in the reference, whose inputs arrive already quantised; it
+ * produces exactly the hidden_states / hidden_states_scale pair of
+ * kernel.py:600-613. Pointers 16-byte aligned (scale: 4-byte). */
+int mi_moe_quantize_fp8(const void* hidden_bf16, int64_t num_tokens, uint8_t* hidden_states,
+                        float* hidden_states_scale, void* stream);
+
 /* Message of the last error on the calling thread ("" if none). */
 const char* mi_moe_last_error(void);
 

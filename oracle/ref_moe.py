@@ -22,6 +22,12 @@ Pinning status (each function's checks live in ``tests/test_oracle.py``):
 * ``moe_forward``     pinned: combine known-answer (two experts, one-hot
                       weights), linearity in the routed scaling factor and
                       in the GEMM2 scales, zero output for empty routing.
+* ``quantize_fp8_blocks`` (the activation quantiser that produces
+                      hidden_states / hidden_states_scale; no reference
+                      code exists for it) pinned: a pure-Python e4m3fn
+                      round-to-nearest-even over all 256 codes, the block
+                      maximum landing exactly on +-448, the rounding-error
+                      bound, zero blocks and a scale-layout probe.
 """
 from __future__ import annotations
 
@@ -112,6 +118,27 @@ def dequant_activations(hs8: torch.Tensor, hs_scale: torch.Tensor, acc_dtype=tor
     T, H = hs8.shape
     full = hs_scale.to(acc_dtype).t().repeat_interleave(BLOCK, 1)[:, :H]
     return hs8.to(acc_dtype) * full
+
+
+FP8_MAX = 448.0  # largest finite e4m3fn value
+QUANT_EPS = 1e-10  # floor of a block's amax, so an all-zero block gets a finite scale
+
+
+def quantize_fp8_blocks(x: torch.Tensor, eps: float = QUANT_EPS):
+    """Per-token, per-128-element-block fp8 e4m3fn quantisation of activations.
+
+    Produces the ``hidden_states`` / ``hidden_states_scale`` pair that
+    ``run`` consumes (kernel.py:600-613), with the scale in the block-major
+    [H/128, T] layout kernel.py:169 reads. In fp32: s = max(amax, eps) / 448,
+    q = e4m3fn(clamp(x / s, -448, 448)) rounded to nearest even.
+    Returns (q [T, H] float8_e4m3fn, s [H/128, T] fp32). Finite inputs only.
+    """
+    T, H = x.shape
+    xf = x.to(torch.float32).reshape(T, H // BLOCK, BLOCK)
+    amax = xf.abs().amax(dim=2)
+    s = torch.clamp(amax, min=eps) / FP8_MAX
+    q = torch.clamp(xf / s[..., None], -FP8_MAX, FP8_MAX).to(torch.float8_e4m3fn)
+    return q.reshape(T, H), s.t().contiguous()
 
 
 def swiglu(g: torch.Tensor) -> torch.Tensor:

@@ -112,6 +112,15 @@ def test_route_rejects_before_launch():
     assert L.mi_moe_route(None, None, 0, 0, 2.5, None, None, None) == _lib.MI_MOE_OK
 
 
+def test_quantize_rejects_before_launch():
+    L = _lib.lib()
+    assert L.mi_moe_quantize_fp8(None, -1, None, None, None) == _lib.MI_MOE_ERR_INVALID
+    assert L.mi_moe_quantize_fp8(None, 0, None, None, None) == _lib.MI_MOE_OK
+    assert L.mi_moe_quantize_fp8(None, 4, None, None, None) == _lib.MI_MOE_ERR_INVALID
+    assert L.mi_moe_quantize_fp8((1 << 20) + 8, 4, 1 << 21, 1 << 22, None) == _lib.MI_MOE_ERR_INVALID
+    assert b"misaligned" in L.mi_moe_last_error()
+
+
 def test_python_wrapper_validates_shapes_and_device():
     T = 4
     good = dict(

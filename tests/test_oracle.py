@@ -237,3 +237,95 @@ def test_tolerance_report_flags_planted_error():
 def test_algorithmic_counts():
     assert R.algorithmic_bytes(0, 32) - 512 == 1_409_630_208
     assert R.algorithmic_flops(1) == 88_080_384
+
+
+# ---------------------------------------------------------------- quantiser
+
+
+def _e4m3fn_value(code: int) -> float:
+    """Decode one e4m3fn byte (bias 7, subnormals, no infinities)."""
+    sign = -1.0 if code & 0x80 else 1.0
+    exp, man = (code >> 3) & 15, code & 7
+    if exp == 15 and man == 7:
+        return math.nan
+    if exp == 0:
+        return sign * man * 2.0 ** -9
+    return sign * (1 + man / 8) * 2.0 ** (exp - 7)
+
+
+def _e4m3fn_rne(v: float) -> int:
+    """Nearest finite e4m3fn code to v, ties to the even code (|v| <= 448)."""
+    best = None
+    for code in range(256):
+        c = _e4m3fn_value(code)
+        if math.isnan(c) or (code == 0x80 and v >= 0) or (code == 0 and v < 0 and math.copysign(1, v) < 0):
+            continue
+        d = abs(v - c)
+        key = (d, code & 1)
+        if best is None or key < best[0]:
+            best = (key, code)
+    return best[1]
+
+
+def test_e4m3fn_rounding_matches_brute_force():
+    # every adjacent pair's midpoint (exact ties), points just off the
+    # midpoints, and random values across the whole range
+    vals = [_e4m3fn_value(c) for c in range(0x7F)]  # non-negative finite codes, ascending
+    pts = []
+    for a, b in zip(vals, vals[1:]):
+        m = (a + b) / 2
+        pts += [m, -m, m * (1 + 2 ** -20), m * (1 - 2 ** -20), a, -b]
+    g = torch.Generator().manual_seed(5)
+    pts += (torch.randn(2000, generator=g) * 40).clamp(-448, 448).tolist()
+    pts += (torch.rand(500, generator=g) * 2 ** -6).tolist()  # subnormal range
+    x = torch.tensor(pts, dtype=torch.float32)
+    got = x.to(torch.float8_e4m3fn).view(torch.uint8).tolist()
+    for v, code in zip(x.tolist(), got):
+        assert code == _e4m3fn_rne(v), (v, hex(code), hex(_e4m3fn_rne(v)))
+
+
+def test_quantize_block_max_hits_448_and_layout():
+    T, H = 3, 512
+    g = torch.Generator().manual_seed(6)
+    x = torch.randn(T, H, generator=g).to(torch.bfloat16)
+    # block (t=2, b=1) gets a much larger magnitude: its scale must land at [1, 2]
+    x[2, 128:256] *= 1000
+    x[1, 256:384] = 0  # an all-zero block
+    q, s = R.quantize_fp8_blocks(x)
+    assert q.dtype == torch.float8_e4m3fn and q.shape == (T, H)
+    assert s.dtype == torch.float32 and s.shape == (H // 128, T)
+    xf = x.float().view(T, H // 128, 128)
+    amax = xf.abs().amax(2)
+    assert torch.equal(s[1, 2], torch.max(amax[2, 1], torch.tensor(1e-10)) / 448)
+    assert s[1, 2] > 100 * s[0, 2] and s[1, 2] > 100 * s[1, 0]
+    qf = q.float().view(T, H // 128, 128)
+    for t in range(T):
+        for b in range(H // 128):
+            if amax[t, b] == 0:
+                assert torch.count_nonzero(qf[t, b]) == 0
+                assert s[b, t] == torch.tensor(1e-10, dtype=torch.float32) / 448
+                continue
+            i = int(xf[t, b].abs().argmax())
+            assert abs(float(qf[t, b, i])) == 448.0
+            assert math.copysign(1, float(qf[t, b, i])) == math.copysign(1, float(xf[t, b, i]))
+
+
+def test_quantize_round_trip_error_bound():
+    T, H = 4, 1024
+    g = torch.Generator().manual_seed(8)
+    x = (torch.randn(T, H, generator=g) * torch.logspace(-3, 3, H // 128).repeat_interleave(128)).to(torch.bfloat16)
+    q, s = R.quantize_fp8_blocks(x)
+    deq = R.dequant_activations(q, s, torch.float64)
+    xd = x.double()
+    sd = s.double().t().repeat_interleave(128, 1)
+    y = xd / sd  # value in fp8 units
+    normal = y.abs() >= 2 ** -6
+    # 3 mantissa bits: half an ulp is 2^-4 relative (normal) or 2^-10 absolute (subnormal)
+    assert ((deq - xd).abs() <= 2 ** -4 * xd.abs() * (1 + 1e-6))[normal].all()
+    assert ((deq - xd).abs() <= 2 ** -10 * sd * (1 + 1e-6))[~normal].all()
+    # a value that is already an fp8 multiple of its block's scale survives exactly
+    z = torch.zeros(1, 128)
+    z[0, 0], z[0, 1], z[0, 2] = 448.0, -3.5, 0.013671875  # 7 * 2^-9 is subnormal
+    q2, s2 = R.quantize_fp8_blocks(z.to(torch.bfloat16))
+    assert float(s2[0, 0]) == 1.0
+    assert torch.equal(q2.float()[0, :3], z[0, :3])
