@@ -77,7 +77,7 @@ Variants pick_variants(int64_t T) {
     // has at most a few row tiles, 64-column GEMM2 waves from T = 64, the
     // LDS-tiled kernels once experts hold hundreds of rows.
     if (T <= 4) v = {5, VARIANT_GEMM2_COMBINE};  // one launch fewer where launches dominate
-    else if (T <= 32) v = {5, 5};
+    else if (T <= 32) v = {9, 5};
     else if (T <= 128) v = {5, 14};
     else if (T <= 256) v = {1, 13};
     else v = {3, 3};
