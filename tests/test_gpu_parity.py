@@ -183,6 +183,29 @@ def test_skew_all_rows_on_biased_experts():
     assert torch.equal(eoff, want)
 
 
+def test_strided_inputs_and_output():
+    """Non-contiguous views (kernel.py:545-546, :733-737 pass explicit strides) give the
+    same bits as contiguous tensors: hidden_states_scale as the transpose of a [T, 56]
+    tensor, routing_logits as a column slice, output as a strided view."""
+    from flashinfer_amd import kernel
+    log("test_strided_inputs_and_output")
+    wl = W.standard("c1_t64")
+    a = run_gpu(wl)
+    args = gpu_args(wl)
+    T = wl.T
+    wide = torch.zeros(T, 512, device="cuda")
+    wide[:, 100:356] = args[0]
+    args[0] = wide[:, 100:356]
+    args[3] = args[3].t().contiguous().t()  # [56, T] view with strides (1, 56)
+    assert not args[0].is_contiguous() and not args[3].is_contiguous()
+    buf = torch.full((T, 2 * 7168), float("nan"), dtype=torch.bfloat16, device="cuda")
+    out = buf[:, ::2]
+    assert not out.is_contiguous()
+    kernel.run(*args, out)
+    torch.cuda.synchronize()
+    assert torch.equal(a.view(torch.int16), out.contiguous().view(torch.int16))
+
+
 def test_scalar_tensor_arguments():
     """Scalars given as 0-d tensors behave like Python numbers (kernel.py:547-548)."""
     from flashinfer_amd import kernel
