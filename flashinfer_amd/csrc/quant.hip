@@ -7,10 +7,12 @@
 // IEEE fp32 (HIP's default correctly rounded divide), so q is bit-identical
 // to the same formula in fp32 on the CPU.
 //
-// One 16-lane DPP row owns one block: each lane loads 8 bf16 (16 bytes), the
-// row max is four xor-shuffles inside the row, and each lane stores 8 fp8
-// bytes, so a row reads 256 contiguous bytes and writes 128. A 256-thread
-// workgroup covers 16 consecutive blocks of the flattened [T * 56] block list.
+// One 16-lane DPP row owns one (token, block): each lane loads 8 bf16 (16
+// bytes), the row max is four xor-shuffles inside the row, and each lane
+// stores 8 fp8 bytes. A 256-thread workgroup covers 16 consecutive tokens and
+// NB blocks per token (all loads issued before any reduction), so the 16
+// scales it writes per block are one contiguous 64-byte run of
+// hidden_states_scale[b, t0 .. t0+15].
 #include "common.hpp"
 
 namespace mimoe {
@@ -21,45 +23,58 @@ constexpr float QUANT_EPS = 1e-10f;
 __device__ __forceinline__ float bf16_lo(uint32_t w) { return __uint_as_float(w << 16); }
 __device__ __forceinline__ float bf16_hi(uint32_t w) { return __uint_as_float(w & 0xffff0000u); }
 
+constexpr int QUANT_NB = 2;  // blocks per token per workgroup (56 / 2 = 28 in y)
+
 __global__ __launch_bounds__(256) void quant_fp8_kernel(const uint16_t* __restrict__ x, int T,
                                                          uint8_t* __restrict__ q,
                                                          float* __restrict__ scale) {
-    const int blk = blockIdx.x * 16 + (threadIdx.x >> 4);  // flattened (token, block)
-    const int sub = threadIdx.x & 15;                      // 8-element slice of the block
-    const bool live = blk < T * HB;                        // uniform across the 16-lane row
-    float v[8];
-    float amax = 0.f;
-    if (live) {
-        const uint4 w = *reinterpret_cast<const uint4*>(x + (size_t)blk * BLK + sub * 8);
-        v[0] = bf16_lo(w.x); v[1] = bf16_hi(w.x);
-        v[2] = bf16_lo(w.y); v[3] = bf16_hi(w.y);
-        v[4] = bf16_lo(w.z); v[5] = bf16_hi(w.z);
-        v[6] = bf16_lo(w.w); v[7] = bf16_hi(w.w);
+    const int t = blockIdx.x * 16 + (threadIdx.x >> 4);  // token of this 16-lane row
+    const int sub = threadIdx.x & 15;                    // 8-element slice of the block
+    const bool live = t < T;                             // uniform across the row
+    float v[QUANT_NB][8];
+    float amax[QUANT_NB];
 #pragma unroll
-        for (int i = 0; i < 8; ++i) amax = fmaxf(amax, fabsf(v[i]));
+    for (int j = 0; j < QUANT_NB; ++j) {
+        amax[j] = 0.f;
+        if (live) {
+            const int b = blockIdx.y + j * (HB / QUANT_NB);
+            const uint4 w = *reinterpret_cast<const uint4*>(x + (size_t)t * H + b * BLK + sub * 8);
+            v[j][0] = bf16_lo(w.x); v[j][1] = bf16_hi(w.x);
+            v[j][2] = bf16_lo(w.y); v[j][3] = bf16_hi(w.y);
+            v[j][4] = bf16_lo(w.z); v[j][5] = bf16_hi(w.z);
+            v[j][6] = bf16_lo(w.w); v[j][7] = bf16_hi(w.w);
+        }
     }
 #pragma unroll
-    for (int m = 8; m >= 1; m >>= 1) amax = fmaxf(amax, __shfl_xor(amax, m, 16));
-    if (!live) return;
-    const float s = fmaxf(amax, QUANT_EPS) / FP8_MAX;
-    uint32_t lo = 0, hi = 0;
+    for (int j = 0; j < QUANT_NB; ++j) {
+        if (live) {
 #pragma unroll
-    for (int i = 0; i < 8; ++i) v[i] = fminf(fmaxf(v[i] / s, -FP8_MAX), FP8_MAX);
-    lo = __builtin_amdgcn_cvt_pk_fp8_f32(v[0], v[1], lo, false);
-    lo = __builtin_amdgcn_cvt_pk_fp8_f32(v[2], v[3], lo, true);
-    hi = __builtin_amdgcn_cvt_pk_fp8_f32(v[4], v[5], hi, false);
-    hi = __builtin_amdgcn_cvt_pk_fp8_f32(v[6], v[7], hi, true);
-    *reinterpret_cast<uint2*>(q + (size_t)blk * BLK + sub * 8) = make_uint2(lo, hi);
-    if (sub == 0) {
-        const int t = blk / HB, b = blk - t * HB;
-        scale[(size_t)b * T + t] = s;
+            for (int i = 0; i < 8; ++i) amax[j] = fmaxf(amax[j], fabsf(v[j][i]));
+        }
+#pragma unroll
+        for (int m = 8; m >= 1; m >>= 1) amax[j] = fmaxf(amax[j], __shfl_xor(amax[j], m, 16));
+    }
+    if (!live) return;
+#pragma unroll
+    for (int j = 0; j < QUANT_NB; ++j) {
+        const int b = blockIdx.y + j * (HB / QUANT_NB);
+        const float s = fmaxf(amax[j], QUANT_EPS) / FP8_MAX;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) v[j][i] = fminf(fmaxf(v[j][i] / s, -FP8_MAX), FP8_MAX);
+        uint32_t lo = 0, hi = 0;
+        lo = __builtin_amdgcn_cvt_pk_fp8_f32(v[j][0], v[j][1], lo, false);
+        lo = __builtin_amdgcn_cvt_pk_fp8_f32(v[j][2], v[j][3], lo, true);
+        hi = __builtin_amdgcn_cvt_pk_fp8_f32(v[j][4], v[j][5], hi, false);
+        hi = __builtin_amdgcn_cvt_pk_fp8_f32(v[j][6], v[j][7], hi, true);
+        *reinterpret_cast<uint2*>(q + (size_t)t * H + b * BLK + sub * 8) = make_uint2(lo, hi);
+        if (sub == 0) scale[(size_t)b * T + t] = s;
     }
 }
 
 hipError_t launch_quant_fp8(const void* x, int T, uint8_t* q, float* scale, hipStream_t s) {
     if (T <= 0) return hipSuccess;
-    const int blocks = T * HB;
-    hipLaunchKernelGGL(quant_fp8_kernel, dim3((blocks + 15) / 16), dim3(256), 0, s,
+    static_assert(HB % QUANT_NB == 0, "blocks per workgroup");
+    hipLaunchKernelGGL(quant_fp8_kernel, dim3((T + 15) / 16, HB / QUANT_NB), dim3(256), 0, s,
                        (const uint16_t*)x, T, q, scale);
     return hipGetLastError();
 }
