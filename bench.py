@@ -216,6 +216,43 @@ def time_quantizer(T, reps=50):
             "hbm_frac": round(nbytes / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4)}
 
 
+def vendor_gemm_reference():
+    """Plain GEMMs of the operator's shapes through the vendor library
+    (torch._scaled_mm -> hipBLASLt for fp8, torch.matmul for bf16): per-tensor
+    scales, contiguous operands, no gather, no block scales, no SwiGLU. A
+    yardstick for the fused grouped kernels, not part of the operator."""
+    dev = "cuda"
+    g = torch.Generator(device=dev).manual_seed(0)
+    rows = []
+
+    def timed(fn, reps=20):
+        fn()
+        e0 = torch.cuda.Event(enable_timing=True)
+        e1 = torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(reps):
+            fn()
+        e1.record()
+        e1.synchronize()
+        return e0.elapsed_time(e1) * 1e3 / reps
+
+    one = torch.tensor(1.0, device=dev)
+    for M in (256, 416, 1024, 4096, 14000):  # GEMM1: [M, 7168] x [4096, 7168]^T, fp8
+        a = torch.randn(M, H, device=dev, generator=g).to(torch.float8_e4m3fn)
+        b = torch.randn(2 * I, H, device=dev, generator=g).to(torch.float8_e4m3fn)
+        us = timed(lambda: torch._scaled_mm(a, b.t(), scale_a=one, scale_b=one,
+                                            out_dtype=torch.bfloat16))
+        rows.append({"gemm": "fp8 M x 4096 x 7168", "M": M, "us": round(us, 1),
+                     "tflops": round(2 * M * 2 * I * H / us / 1e6, 1)})
+    for M in (416, 4096, 14000):  # GEMM2: [M, 2048] x [7168, 2048]^T, bf16
+        a = torch.randn(M, I, device=dev, generator=g, dtype=torch.bfloat16)
+        b = torch.randn(H, I, device=dev, generator=g, dtype=torch.bfloat16)
+        us = timed(lambda: a @ b.t())
+        rows.append({"gemm": "bf16 M x 7168 x 2048", "M": M, "us": round(us, 1),
+                     "tflops": round(2 * M * H * I / us / 1e6, 1)})
+    return rows
+
+
 def measured_peaks():
     """Achievable rates on this GPU, from the probes in libmi_peaks.so
     (include/mi_peaks.h): an HBM read and copy (best workgroup count of a
@@ -360,6 +397,9 @@ def main():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-pmc", action="store_true",
                     help="skip the rocprofv3 FETCH_SIZE / WRITE_SIZE passes (traffic = null)")
+    ap.add_argument("--vendor-gemm-ref", action="store_true",
+                    help="only time plain vendor-library GEMMs of the operator's shapes and "
+                         "print them as one JSON line")
     ap.add_argument("--copy-calib-mib", type=int, default=0,
                     help="(counter passes) copy this many MiB device-to-device before timing")
     a = ap.parse_args()
@@ -369,12 +409,15 @@ def main():
               "Run with --gpus 1.", file=sys.stderr)
         sys.exit(2)
     traffic = None
-    if not a.no_pmc:
+    if not a.no_pmc and not a.vendor_gemm_ref:
         # counter passes run as child processes before this one uses the GPU
         traffic = pmc_traffic(a.workload, "gemm1_")
     if not torch.cuda.is_available():
         print("bench.py needs a ROCm GPU", file=sys.stderr)
         sys.exit(2)
+    if a.vendor_gemm_ref:
+        print(json.dumps({"vendor_gemm_reference": vendor_gemm_reference()}), flush=True)
+        return
     if a.copy_calib_mib > 0:
         src = torch.empty(a.copy_calib_mib << 20, dtype=torch.uint8, device="cuda")
         dst = torch.empty_like(src)
