@@ -12,8 +12,9 @@ bracketed by ``torch.cuda.synchronize()``; ``value`` is the median trial's
 microseconds per call. A second pass of 5 x K calls records HIP events
 between the five kernels on the stream they run on, which gives each
 kernel's average duration. A third pass times single calls with the caches
-cold (a 512 MiB read before each call evicts the MALL and L2s), and the
-probes of libmi_peaks.so measure the HBM and MFMA rates this GPU achieves.
+cold (a 512 MiB read before each call evicts the MALL and L2s), a fourth
+replays the call captured in a HIP graph, and the probes of libmi_peaks.so
+measure the HBM and MFMA rates this GPU achieves.
 
 Rank 0 prints ONE JSON line. ``roofline`` covers the dominant kernel
 (GEMM1+SwiGLU at decode); ``call_roofline`` the whole call; ``sweep`` the
@@ -135,6 +136,7 @@ def time_workload(wl, steps, warmup, trials=5):
                 phase_sum[p] += ev[k][p].elapsed_time(ev[k][p + 1]) * 1e3
     phase_us = [s / (steps * trials) for s in phase_sum]
     cold_us = time_cold(args, out, min(steps, 20))
+    graph_us = time_graph(args, out, steps)
     us = statistics.median(trial_us)
     B = call_bytes(wl.T, A_e)
     F1, F2 = S * GEMM1_FLOPS_PER_SLOT, S * GEMM2_FLOPS_PER_SLOT
@@ -155,6 +157,7 @@ def time_workload(wl, steps, warmup, trials=5):
         "roofline_frac": round(bound_t / t, 4),
         "mixed_roofline_frac": round(mixed_t / t, 4),
         "us_per_call_cold": round(cold_us, 2),
+        "us_per_call_graph": round(graph_us, 2),
         "algorithmic_bytes": B, "algorithmic_flops": F,
         "phase_us": {n: round(v, 2) for n, v in zip(_lib.PHASES, phase_us)},
     }
@@ -166,6 +169,32 @@ def time_workload(wl, steps, warmup, trials=5):
     res["gemm2_tflops"] = round(F2 / g2 / 1e12, 2) if g2 > 0 else None
     del args, out
     return res
+
+
+def time_graph(args, out, steps, trials=5):
+    """Median microseconds per call when the call is captured once in a HIP
+    graph and replayed (launch overheads of the five kernels shrink)."""
+    from flashinfer_amd import kernel
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        kernel.run(*args, out)
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        kernel.run(*args, out)
+    g.replay()
+    torch.cuda.synchronize()
+    ts = []
+    for _ in range(trials):
+        t0 = time.perf_counter()
+        for _ in range(steps):
+            g.replay()
+        torch.cuda.synchronize()
+        ts.append((time.perf_counter() - t0) * 1e6 / steps)
+    del g
+    return statistics.median(ts)
 
 
 def time_cold(args, out, steps, flush_mib=512):
@@ -485,6 +514,7 @@ def main():
                           "tflops": head["tflops"], "roofline_frac": head["roofline_frac"],
                           "mixed_roofline_frac": head["mixed_roofline_frac"],
                           "us_per_call_cold": head["us_per_call_cold"],
+                          "us_per_call_graph": head["us_per_call_graph"],
                           "phase_us": head["phase_us"]},
         "traffic_detail": traffic,
         "cpu_baseline": cpu,

@@ -1,0 +1,87 @@
+"""Serving-style use of the operator: concurrent calls on two streams (each
+stream caches its own workspace) and HIP graph capture + replay (the call
+allocates nothing and never synchronises, so it is capturable once warm).
+Every result is compared bitwise with a plain eager call on the same inputs."""
+import pytest
+import torch
+
+from _helpers import gpu_args, log, run_gpu
+
+from flashinfer_amd import kernel
+from flashinfer_amd import workloads as W
+
+pytestmark = pytest.mark.gpu
+H = 7168
+
+
+def _bits(x):
+    return x.view(torch.int16).cpu()
+
+
+def test_two_streams_concurrently():
+    log("test_two_streams_concurrently")
+    wa, wb = W.standard("c1_t64"), W.standard("t256")
+    ref_a, ref_b = run_gpu(wa), run_gpu(wb)
+    args_a, args_b = gpu_args(wa), gpu_args(wb)
+    out_a = torch.empty(wa.T, H, dtype=torch.bfloat16, device="cuda")
+    out_b = torch.empty(wb.T, H, dtype=torch.bfloat16, device="cuda")
+    sa, sb = torch.cuda.Stream(), torch.cuda.Stream()
+    torch.cuda.synchronize()
+    for _ in range(3):
+        with torch.cuda.stream(sa):
+            kernel.run(*args_a, out_a)
+        with torch.cuda.stream(sb):
+            kernel.run(*args_b, out_b)
+    torch.cuda.synchronize()
+    assert torch.equal(_bits(out_a), _bits(ref_a))
+    assert torch.equal(_bits(out_b), _bits(ref_b))
+
+
+@pytest.mark.parametrize("name,other", [("c1_t64", "c0_t16"), ("c2_t1024_o0", "c2_t1024_o64")])
+def test_graph_capture_and_replay(name, other):
+    """Capture one call, then replay it on fresh inputs copied into the captured
+    tensors; every replay must equal an eager call on the same inputs."""
+    log(f"test_graph_capture_and_replay[{name}]")
+    wl = W.standard(name)
+    static = gpu_args(wl)
+    out = torch.empty(wl.T, H, dtype=torch.bfloat16, device="cuda")
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):  # warm up: workspace and code objects outside the capture
+        kernel.run(*static, out)
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        kernel.run(*static, out)
+    torch.cuda.synchronize()
+
+    # inputs of the same shape: the original tokens, then tokens of another
+    # workload truncated/padded to T (routing and activations change)
+    alt = W.standard(other)
+    variants = [wl.tensors]
+    t2 = {k: v for k, v in wl.tensors.items()}
+    n = min(wl.T, alt.T)
+    for key in ("routing_logits", "hidden_states"):
+        x = wl.tensors[key].clone()
+        x[:n] = alt.tensors[key][:n]
+        t2[key] = x
+    s2 = wl.tensors["hidden_states_scale"].clone()
+    s2[:, :n] = alt.tensors["hidden_states_scale"][:, :n]
+    t2["hidden_states_scale"] = s2
+    variants.append(t2)
+    variants.append(wl.tensors)
+    for i, t in enumerate(variants):
+        static[0].copy_(t["routing_logits"])
+        static[2].copy_(t["hidden_states"])
+        static[3].copy_(t["hidden_states_scale"])
+        out.fill_(float("nan"))
+        g.replay()
+        torch.cuda.synchronize()
+        got = out.clone()
+        eager = torch.empty_like(out)
+        kernel.run(*static, eager)  # the program's own eager work between replays
+        torch.cuda.synchronize()
+        log(f"  replay {i}: equal={torch.equal(_bits(got), _bits(eager))}")
+        assert torch.isfinite(got.float()).all()
+        assert torch.equal(_bits(got), _bits(eager))
