@@ -1,8 +1,8 @@
 """CPU restatement of the FP8 block-scaled DeepSeek-routed fused MoE.
 
 TEST INFRASTRUCTURE ONLY: imported by ``tests/``, ``__graft_entry__.smoke()``
-and ``bench.py``'s ``cpu_baseline`` leg, as the checker. Never on the product
-path.
+and ``bench.py``'s ``cpu_baseline`` leg, as the answer GPU results are compared
+with (or the timed CPU baseline). Never on the product path.
 
 It restates the definition ``moe_fp8_block_scale_ds_routing_topk8_ng8_kg4_e32_h7168_i2048``
 (config.toml:3) as the Triton solution in ``solution/triton/kernel.py``
