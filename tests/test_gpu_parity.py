@@ -183,6 +183,19 @@ def test_skew_all_rows_on_biased_experts():
     assert torch.equal(eoff, want)
 
 
+# Both sides of every T at which the default kernels change: fused GEMM2+combine
+# (T <= 4), fused route+sort (T <= 8), GEMM1/GEMM2 streaming shapes (32, 128),
+# LDS-tiled GEMMs (> 256), chunked two-kernel sort (> 1024).
+@pytest.mark.parametrize("T", [2, 5, 8, 9, 32, 33, 128, 129, 256, 257, 1024, 1025, 2049])
+def test_variant_boundaries(T):
+    log(f"test_variant_boundaries[T={T}]")
+    wl = W.make_workload(f"boundary_t{T}", T=T, seed=1000 + T, local_expert_offset=32 * (T % 8))
+    _route_check(wl)
+    out = run_gpu(wl, fill=float("nan"))
+    assert torch.isfinite(out.float()).all()
+    _check_output(wl, out, spread_tokens(wl.T, 96))
+
+
 def test_strided_inputs_and_output():
     """Non-contiguous views (kernel.py:545-546, :733-737 pass explicit strides) give the
     same bits as contiguous tensors: hidden_states_scale as the transpose of a [T, 56]
