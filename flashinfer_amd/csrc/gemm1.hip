@@ -9,10 +9,11 @@
 // 128-wide scale block, so the product of the two block scales is applied
 // to each MFMA result in the fp32 accumulator (kernel.py:168-171).
 //
-// "Stream" variant: weight tiles are not reused across row tiles, so they go
-// global -> VGPR with a D-deep register prefetch ring instead of through LDS.
-// A workgroup is 4 waves; wave w owns gate columns j0..j0+15 and the matching
-// up columns I+j0..I+j0+15 for the BM = 16*MT rows of one expert's row tile.
+// "Stream" variant (template <MT, D, NW>): weight tiles are not reused across
+// row tiles, so they go global -> VGPR with a D-deep register prefetch ring
+// instead of through LDS. A workgroup is NW waves; wave w owns gate columns
+// j0..j0+15 and the matching up columns I+j0..I+j0+15 for the BM = 16*MT rows
+// of one expert's row tile.
 //
 // Operand layout: lane l feeds row (l % 16) of a 16x128 operand with bytes
 // [16g, 16g+16) and [64+16g, 64+16g+16) of the 128-byte k-block, g = l / 16.

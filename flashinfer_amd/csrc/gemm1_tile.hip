@@ -194,8 +194,6 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm1_tile_kernel(
     }
 }
 
-int gemm1_tile_bm(int variant) { return variant == 3 ? 256 : 128; }
-
 hipError_t launch_gemm1_tile(const Plan& p, const uint8_t* hs, const float* hs_scale,
                              const uint8_t* w1, const float* w1s, int variant, hipStream_t s) {
     if (variant == 3) {

@@ -11,9 +11,10 @@
 // requantised to fp8, whose 3-bit mantissa would put the output outside a
 // 1e-2 relative tolerance.
 //
-// Stream variant: 4 waves, each wave owns 32 output columns (two 16-column
-// sub-tiles) so a workgroup covers one 128-column scale block; weights go
-// global -> VGPR through a D-deep prefetch ring.
+// Stream variant (template <MT, D, NW, NQ>): NW waves per workgroup, each
+// owning NQ 16-column sub-tiles (16 * NQ output columns, inside one 128-column
+// scale block) for 16 * MT slots of one expert; weights go global -> VGPR
+// through a D-deep prefetch ring.
 //
 // Operand layout: lane l (row l % 16, g = l / 16) loads bytes [16g, 16g+16)
 // and [64+16g, 64+16g+16) of the 128-wide k-block of its weight row; MFMA h
