@@ -77,11 +77,15 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm1_tile_kernel(
         sa_off = (uint32_t)p.sorted_tok[row0 + min(row, nrows - 1)];
     }
 
+    // Copies whose 8 rows all lie past the expert's last row are skipped
+    // (wave-uniform): those LDS rows only feed MFMA rows that are never
+    // stored, and at medium T most of a 256-row tile is such rows.
     auto issue = [&](int stage, int kb) __attribute__((always_inline)) {
         uint8_t* s = smem + stage * C::STAGE;
 #pragma unroll
         for (int i = 0; i < C::A_LD; ++i)
-            g2l16(hs + a_off[i] + kb * BLK, s + (wave * C::A_LD + i) * 1024);
+            if (8 * (wave * C::A_LD + i) < nrows)
+                g2l16(hs + a_off[i] + kb * BLK, s + (wave * C::A_LD + i) * 1024);
 #pragma unroll
         for (int i = 0; i < C::B_LD; ++i)
             g2l16(w1 + b_off[i] + kb * BLK, s + C::A_BYTES + (wave * C::B_LD + i) * 1024);

@@ -1,0 +1,206 @@
+// Grouped FP8 GEMM1 + SwiGLU for medium row counts per expert ("wide" tiles).
+//
+// Same contract as gemm1_stream_kernel (solution/triton/kernel.py:69-186 and
+// :301-330): act[s, j] = silu(G[s, I+j]) * G[s, j] with
+//   G[s, n] = sum_kb sa[kb, tok(s)] * sb1[e, n/128, kb] * (A8[tok(s), kb-block] . W1[e, n, kb-block]).
+//
+// Shape (template <MTW, D, DA>): a workgroup of 4 waves owns BM = 16*MTW rows
+// of one expert and 64 gate columns plus the 64 matching up columns; wave w
+// owns gate columns j0..j0+15 (and up I+j0..) for all BM rows, so no two
+// waves need the same weight bytes. Weights therefore go global -> VGPR
+// through a D-deep register ring per wave (as in the stream kernel), while
+// the BM gathered activation rows of a k-block, which every wave needs, are
+// loaded once per workgroup into a DA-deep register staging ring and written
+// to an LDS double buffer one k-block ahead of their use, together with the
+// combined scales sa*sb (one product per row and half, computed once per
+// workgroup from the tile's activation scales, which sit in LDS for the
+// whole kernel): one barrier per k-block.
+//
+// All loads are ordinary compiler-visible loads, so the compiler's memory
+// counters stay exact and a load waits only for its own data.
+//
+// Operand layout as in the stream kernel: lane l feeds row (l % 16) of a
+// 16x128 operand with bytes [16g, 16g+16) and [64+16g, 64+16g+16) of the
+// k-block, g = l / 16. LDS rows are 128 bytes with chunk c of row r at
+// position c ^ swz8(r).
+#include "tile_common.hpp"
+
+namespace mimoe {
+
+constexpr int gcd_c(int a, int b) { return b == 0 ? a : gcd_c(b, a % b); }
+constexpr int lcm_c(int a, int b) { return a / gcd_c(a, b) * b; }
+
+constexpr int WIDE_NW = 4;                  // waves per workgroup
+constexpr int WIDE_G = 16 * WIDE_NW;        // gate columns per workgroup
+
+template <int MTW, int D, int DA>
+__global__ __launch_bounds__(64 * WIDE_NW) void gemm1_wide_kernel(Plan p, const uint8_t* __restrict__ hs,
+                                                                  const float* __restrict__ hs_scale,
+                                                                  const uint8_t* __restrict__ w1,
+                                                                  const float* __restrict__ w1s) {
+    constexpr int BM = 16 * MTW;
+    constexpr int THREADS = 64 * WIDE_NW;
+    constexpr int ROWS_PER_PASS = THREADS / 8;  // 8 threads x 16 B cover one 128-byte row
+    constexpr int A_LD = BM / ROWS_PER_PASS;    // 16-byte loads per thread per k-block
+    static_assert(BM % ROWS_PER_PASS == 0 && BM <= THREADS, "activation loader");
+    static_assert(HB % D == 0 && HB % DA == 0, "ring depths must divide the k-block count");
+    __shared__ __attribute__((aligned(16))) uint8_t a_lds[2][BM * BLK];
+    __shared__ float sa_lds[HB][BM];  // activation scales of the tile's rows, all k-blocks
+    __shared__ __attribute__((aligned(16))) float cs_lds[2][2][BM];  // [buffer][gate, up][row]
+
+    int e, row0, nrows;
+    if (!find_tile(p.meta, META_MTILE1, blockIdx.y, BM, e, row0, nrows)) return;
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int jb = blockIdx.x * WIDE_G;  // first gate column of the workgroup
+    const int j0 = jb + wave * 16;       // first gate column of this wave
+    const int r = lane & 15, g = lane >> 4;
+
+    // weight fragments of this wave (gate and up rows of W1[e])
+    const uint8_t* bg_ptr = w1 + ((size_t)e * N1 + j0 + r) * H + g * 16;
+    const uint8_t* bu_ptr = w1 + ((size_t)e * N1 + I + j0 + r) * H + g * 16;
+    // 64 gate columns lie inside one 128-column scale block, as do the up ones
+    const float* sbg_ptr = w1s + ((size_t)e * N1B + jb / BLK) * HB;
+    const float* sbu_ptr = w1s + ((size_t)e * N1B + (I + jb) / BLK) * HB;
+
+    // activation loader: thread t copies chunk t%8 of rows t/8 + 32i
+    const int ac = tid & 7;
+    const uint8_t* a_src[A_LD];
+    uint32_t a_dst[A_LD];
+#pragma unroll
+    for (int i = 0; i < A_LD; ++i) {
+        const int row = (tid >> 3) + ROWS_PER_PASS * i;
+        a_src[i] = hs + (size_t)p.sorted_tok[row0 + min(row, nrows - 1)] * H + ac * 16;
+        a_dst[i] = row * BLK + ((ac ^ swz8(row)) << 4);
+    }
+
+    v8i bg[D], bu[D];
+    v4i ast[DA][A_LD];
+    float sgs[DA], sus[DA];  // weight scales of the staged k-blocks (uniform)
+    v4f accg[MTW], accu[MTW];
+    const v4f zero = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int m = 0; m < MTW; ++m) { accg[m] = zero; accu[m] = zero; }
+
+    auto load_w = [&](int d, int kb) __attribute__((always_inline)) {
+        bg[d] = ld_frag(bg_ptr + kb * BLK);
+        bu[d] = ld_frag(bu_ptr + kb * BLK);
+    };
+    auto load_a = [&](int s, int kb) __attribute__((always_inline)) {
+#pragma unroll
+        for (int i = 0; i < A_LD; ++i) ast[s][i] = ld16(a_src[i] + kb * BLK);
+        sgs[s] = sbg_ptr[kb];
+        sus[s] = sbu_ptr[kb];
+    };
+    auto store_a = [&](int s, int buf, int kb) __attribute__((always_inline)) {
+#pragma unroll
+        for (int i = 0; i < A_LD; ++i)
+            *reinterpret_cast<v4i*>(&a_lds[buf][a_dst[i]]) = ast[s][i];
+        if (tid < BM) {
+            const float sa = sa_lds[kb][tid];
+            cs_lds[buf][0][tid] = sa * sgs[s];
+            cs_lds[buf][1][tid] = sa * sus[s];
+        }
+    };
+    auto compute = [&](int d, int buf) __attribute__((always_inline)) {
+        const uint8_t* sA = a_lds[buf];
+#pragma unroll
+        for (int m = 0; m < MTW; ++m) {
+            const int row = m * 16 + r;
+            const uint8_t* base = sA + row * BLK;
+            const int sw = swz8(row);
+            const v4i lo = lds16(base + ((g ^ sw) << 4));
+            const v4i hi = lds16(base + (((g + 4) ^ sw) << 4));
+            const v8i a = (v8i){lo.x, lo.y, lo.z, lo.w, hi.x, hi.y, hi.z, hi.w};
+            const v4f pg = mfma_f8_16x16x128(a, bg[d], zero);
+            const v4f pu = mfma_f8_16x16x128(a, bu[d], zero);
+            const float4 sg = *reinterpret_cast<const float4*>(&cs_lds[buf][0][m * 16 + g * 4]);
+            const float4 su = *reinterpret_cast<const float4*>(&cs_lds[buf][1][m * 16 + g * 4]);
+            accg[m][0] += pg[0] * sg.x; accg[m][1] += pg[1] * sg.y;
+            accg[m][2] += pg[2] * sg.z; accg[m][3] += pg[3] * sg.w;
+            accu[m][0] += pu[0] * su.x; accu[m][1] += pu[1] * su.y;
+            accu[m][2] += pu[2] * su.z; accu[m][3] += pu[3] * su.w;
+        }
+        // The products are pure arithmetic, which the compiler would
+        // otherwise sink below the following barriers into the last unrolled
+        // k-block, keeping every LDS fragment of the unrolled body live.
+        // Naming the accumulators here pins each k-block's work before its
+        // barrier.
+#pragma unroll
+        for (int m = 0; m < MTW; ++m) asm volatile("" : "+v"(accg[m]), "+v"(accu[m]));
+    };
+
+    // Activation scales of every k-block into LDS once: in the loop they come
+    // from LDS, so no vector load there waits on anything but its own data.
+    for (int i = tid; i < HB * BM; i += THREADS) {
+        const int kb = i / BM, m = i % BM;
+        sa_lds[kb][m] = hs_scale[(size_t)kb * p.T + p.sorted_tok[row0 + min(m, nrows - 1)]];
+    }
+    __syncthreads();
+
+    // Prologue: the loads that iterations -D..-1 of the loop would have
+    // issued, in their order (iteration j loads A(j+1+DA), then W(j+D); the
+    // store of A(0) to LDS buffer 0 belongs to iteration -1), so every wait in
+    // the loop sees as many younger loads on the first trip as on later ones.
+    static_assert(D > DA, "prologue order");
+    // (sched_barrier keeps the scheduler from reordering the groups.)
+#pragma unroll
+    for (int d = 0; d < D; ++d) {
+        const int a = d - (D - DA - 1);
+        if (a >= 0) {
+            if (a == DA) store_a(0, 0, 0);  // frees staging slot 0 for A(DA)
+            load_a(a % DA, a);
+            __builtin_amdgcn_sched_barrier(0);
+        }
+        load_w(d, d);
+        __builtin_amdgcn_sched_barrier(0);
+    }
+    __syncthreads();
+
+    // k-block kb: stage kb+1 into the other LDS buffer (its staging slot is
+    // refilled with kb+1+DA), consume kb, refill the weight ring with kb+D.
+    // Loads past the last k-block re-read the last one; their values are
+    // never consumed.
+    constexpr int U = lcm_c(lcm_c(D, DA), 2);  // ring slots and LDS buffer repeat every U
+    static_assert(HB % U == 0, "unroll");
+#pragma unroll 1
+    for (int kb0 = 0; kb0 < HB; kb0 += U) {
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            const int kb = kb0 + u;
+            const int buf = u & 1;
+            const int s = (u + 1) % DA;  // staging slot holding k-block kb+1
+            if (kb + 1 < HB) {
+                store_a(s, buf ^ 1, kb + 1);
+                load_a(s, min(kb + 1 + DA, HB - 1));
+            }
+            compute(u % D, buf);
+            load_w(u % D, min(kb + D, HB - 1));
+            __syncthreads();
+        }
+    }
+
+#pragma unroll
+    for (int m = 0; m < MTW; ++m) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int row = m * 16 + g * 4 + i;
+            if (row < nrows) {
+                const float v = silu(accu[m][i]) * accg[m][i];
+                p.act[(size_t)(row0 + row) * I + j0 + r] = f2bf(v);
+            }
+        }
+    }
+}
+
+hipError_t launch_gemm1_wide(const Plan& p, const uint8_t* hs, const float* hs_scale,
+                             const uint8_t* w1, const float* w1s, hipStream_t s) {
+    dim3 grid(I / WIDE_G, max_mtiles(p.T, 128));
+    hipLaunchKernelGGL((gemm1_wide_kernel<8, 4, 2>), grid, dim3(64 * WIDE_NW), 0, s, p, hs,
+                       hs_scale, w1, w1s);
+    return hipGetLastError();
+}
+
+}  // namespace mimoe

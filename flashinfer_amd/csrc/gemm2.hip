@@ -117,8 +117,20 @@ __global__ __launch_bounds__(64 * NW) void gemm2_stream_kernel(Plan p, const uin
             load(d, kb0 + d + D);
         }
     }
+    // Routing weights of this lane's rows, loaded while the last D k-blocks
+    // are consumed (the asm below keeps them from being sunk into the
+    // per-row stores, where each would wait on its own load).
+    float wrow[MT][4];
+#pragma unroll
+    for (int i = 0; i < MT; ++i)
+#pragma unroll
+        for (int rr = 0; rr < 4; ++rr) wrow[i][rr] = p.sorted_w[row0 + min(i * 16 + g * 4 + rr, nrows - 1)];
 #pragma unroll
     for (int d = 0; d < D; ++d) compute(d, IB - D + d);
+#pragma unroll
+    for (int i = 0; i < MT; ++i)
+#pragma unroll
+        for (int rr = 0; rr < 4; ++rr) asm volatile("" : "+v"(wrow[i][rr]));
 
     // Epilogue: weight each slot's row by its routing weight (kernel.py:364)
     // and store bf16 for the combine.
@@ -128,7 +140,7 @@ __global__ __launch_bounds__(64 * NW) void gemm2_stream_kernel(Plan p, const uin
         for (int rr = 0; rr < 4; ++rr) {
             const int m = i * 16 + g * 4 + rr;
             if (m < nrows) {
-                const float w = p.sorted_w[row0 + m];
+                const float w = wrow[i][rr];
                 uint16_t* dst = p.part + (size_t)(row0 + m) * H + n0 + r;
 #pragma unroll
                 for (int q = 0; q < NQ; ++q) dst[16 * q] = f2bf(w * acc[i][q][rr]);
@@ -146,6 +158,7 @@ int gemm2_bm(int variant) {
         case 4: return 64;
         case 7: return 32;
         case 12: return 32;
+        case 15: return 128;  // the large LDS tile (GEMM2 has no wide kernel)
         default: return 16;
     }
 }
@@ -160,6 +173,7 @@ hipError_t launch_gemm2(const Plan& p, const uint8_t* w2, const float* w2s, int 
                         hipStream_t s) {
     if (p.T <= 0) return hipSuccess;
     if (variant >= 3 && variant <= 4) return launch_gemm2_tile(p, w2, w2s, variant, s);
+    if (variant == 15) return launch_gemm2_tile(p, w2, w2s, 3, s);
     switch (variant) {
         case 0: launch_stream2<1, 4, 4, 2>(p, w2, w2s, s); break;
         case 1: launch_stream2<2, 4, 4, 2>(p, w2, w2s, s); break;

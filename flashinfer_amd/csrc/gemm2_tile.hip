@@ -45,6 +45,7 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm2_tile_kernel(Plan p,
                                                                   const float* __restrict__ w2s) {
     using C = G2Tile<WM, WN>;
     __shared__ __attribute__((aligned(1024))) uint8_t smem[2 * C::STAGE];
+    __shared__ float w_lds[C::THREADS];  // routing weights of the tile's rows (first BM used)
 
     int e, row0, nrows, nt;
     if (!tile_coords<C::NT, GM>(p.meta, META_MTILE2, C::BM, e, row0, nrows, nt)) return;
@@ -71,11 +72,15 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm2_tile_kernel(Plan p,
         b_off[i] = (uint32_t)((e * H + n0 + row) * I + c * 16);
     }
 
+    // Copies whose 4 rows all lie past the expert's last row are skipped
+    // (wave-uniform): those LDS rows only feed output rows that are never
+    // stored.
     auto issue = [&](int stage, int kb) __attribute__((always_inline)) {
         uint8_t* s = smem + stage * C::STAGE;
 #pragma unroll
         for (int i = 0; i < C::A_LD; ++i)
-            g2l16(act + (size_t)a_off[i] + kb * (BLK * 2), s + (wave * C::A_LD + i) * 1024);
+            if (4 * (wave * C::A_LD + i) < nrows)
+                g2l16(act + (size_t)a_off[i] + kb * (BLK * 2), s + (wave * C::A_LD + i) * 1024);
 #pragma unroll
         for (int i = 0; i < C::B_LD; ++i)
             g2l16(w2 + b_off[i] + kb * BLK, s + C::A_BYTES + (wave * C::B_LD + i) * 1024);
@@ -92,14 +97,25 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm2_tile_kernel(Plan p,
 #pragma unroll
         for (int n = 0; n < 4; ++n) acc[m][n] = zero;
 
+    // Routing weights go to LDS with the first stage (one wait for both), so
+    // the epilogue does not wait on a load per row.
+    const float w_row = p.sorted_w[row0 + min(tid, nrows - 1)];
     issue(0, 0);
     wait_vmem();
+    w_lds[tid] = w_row;
     __syncthreads();
 
 #pragma unroll 1
     for (int kb = 0; kb < IB; ++kb) {
         const int cur = kb & 1;
         if (kb + 1 < IB) issue(cur ^ 1, kb + 1);
+        // Waves whose 64 rows lie past the expert's last row only copy
+        // (wave-uniform branch).
+        if (wm * 64 >= nrows) {
+            wait_vmem();
+            __syncthreads();
+            continue;
+        }
         const uint8_t* sA = smem + cur * C::STAGE;
         const uint8_t* sB = sA + C::A_BYTES;
         const float sb = sb_p[kb];
@@ -160,7 +176,7 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm2_tile_kernel(Plan p,
         for (int i = 0; i < 4; ++i) {
             const int row = wm * 64 + m * 16 + g * 4 + i;
             if (row < nrows) {
-                const float w = p.sorted_w[row0 + row];
+                const float w = w_lds[row];
                 uint16_t* dst = p.part + (size_t)(row0 + row) * H + n0 + wn * 64 + r;
 #pragma unroll
                 for (int n = 0; n < 4; ++n) dst[n * 16] = f2bf(w * acc[m][n][i]);

@@ -15,10 +15,11 @@
 // counts are scanned in LDS, and a lane's slot is chunk base + wave prefix +
 // popcount of the lower lanes' ballot bits.
 //
-// Three entry shapes: one workgroup for T <= 1024 (sort_kernel); the same
-// with the routing done in place for small T (route_sort_kernel, one launch
-// for the whole front end); and for large T a per-chunk count kernel plus a
-// per-chunk place kernel that scans the chunk totals itself.
+// Entry shapes: one wave for T <= 64 (sort_small_kernel); one workgroup for
+// T <= 1024 (sort_kernel); either with the routing done in place for small T
+// (route_sort_kernel, one launch for the whole front end); and for large T a
+// per-chunk count kernel plus a per-chunk place kernel that scans the chunk
+// totals itself.
 #include "route_impl.hpp"
 
 namespace mimoe {
@@ -174,6 +175,49 @@ __device__ void sort_one_workgroup(const Plan& p, const int* ids_base, const flo
     place_with_prefix(p, tid, valid, tl, wcnt, lane, wave);
 }
 
+// T <= 64: one wave holds every token (lane t = token t). The expert counts
+// are popcounts of 32 ballots, the offsets a shuffle scan and the placement a
+// second round of ballots: no LDS and no barrier. Same slot order as
+// sort_one_workgroup (token-ascending inside an expert).
+constexpr int SMALL_T = 64;
+
+__device__ void sort_one_wave(const Plan& p, const int* ids_base, const float* w_base, int bm1,
+                              int bm2, int lane) {
+    const bool valid = lane < p.T;
+    const TokLocal tl = load_local(ids_base, w_base, lane, valid, p.local_offset);
+    int cnt = 0;
+#pragma unroll
+    for (int e = 0; e < EL; ++e) {
+        const unsigned long long bal = __ballot((tl.m >> e) & 1u);
+        if (lane == e) cnt = __popcll(bal);
+    }
+    const int off = scan_counts(p, lane, cnt, bm1, bm2, true);
+    const unsigned long long lower = (1ull << lane) - 1ull;
+    int j = 0;
+#pragma unroll
+    for (int e = 0; e < EL; ++e) {
+        const bool hit = (tl.m >> e) & 1u;
+        const unsigned long long bal = __ballot(hit);
+        const int base = __builtin_amdgcn_readlane(off, e);
+        if (hit) {
+            const int pos = base + __popcll(bal & lower);
+            float w = 0.f;
+#pragma unroll
+            for (int k = 0; k < TOPK; ++k) w = (tl.lid[k] == e) ? tl.lw[k] : w;
+            p.sorted_tok[pos] = lane;
+            p.sorted_w[pos] = w;
+            p.tok_slot[(size_t)lane * TOPK + j] = pos;
+            ++j;
+        }
+    }
+    if (valid)
+        for (; j < TOPK; ++j) p.tok_slot[(size_t)lane * TOPK + j] = -1;
+}
+
+__global__ __launch_bounds__(64) void sort_small_kernel(Plan p, int bm1, int bm2) {
+    sort_one_wave(p, p.topk_ids, p.topk_w, bm1, bm2, threadIdx.x);
+}
+
 __global__ __launch_bounds__(1024) void sort_kernel(Plan p, int bm1, int bm2) {
     __shared__ int wcnt[CHUNK / 64][EL];
     sort_one_workgroup(p, p.topk_ids, p.topk_w, bm1, bm2, wcnt);
@@ -181,7 +225,7 @@ __global__ __launch_bounds__(1024) void sort_kernel(Plan p, int bm1, int bm2) {
 
 // Routing + sort in one launch for small T: the 16 waves route the tokens
 // round-robin (global top-k also written for parity checks), then sort from
-// the LDS copy.
+// the LDS copy (one wave for T <= 64).
 constexpr int ROUTE_SORT_MAX_T = 256;
 
 __global__ __launch_bounds__(1024) void route_sort_kernel(Plan p, const float* __restrict__ logits,
@@ -211,6 +255,10 @@ __global__ __launch_bounds__(1024) void route_sort_kernel(Plan p, const float* _
         }
     }
     __syncthreads();
+    if (p.T <= SMALL_T) {
+        if (wave == 0) sort_one_wave(p, s_ids, s_w, bm1, bm2, lane);
+        return;
+    }
     sort_one_workgroup(p, s_ids, s_w, bm1, bm2, wcnt);
 }
 
@@ -272,6 +320,10 @@ hipError_t launch_route_sort(const Plan& p, const float* logits, const void* bia
 hipError_t launch_sort(const Plan& p, int bm1, int bm2, hipStream_t s) {
     if (p.T <= 0) return hipSuccess;
     const int nchunks = sort_chunks(p.T);
+    if (p.T <= SMALL_T) {
+        hipLaunchKernelGGL(sort_small_kernel, dim3(1), dim3(64), 0, s, p, bm1, bm2);
+        return hipGetLastError();
+    }
     if (nchunks == 1) {
         hipLaunchKernelGGL(sort_kernel, dim3(1), dim3(CHUNK), 0, s, p, bm1, bm2);
         return hipGetLastError();
