@@ -18,7 +18,7 @@ CSRC = os.path.join(HERE, "csrc")
 BUILD = os.path.join(HERE, "_build")
 LIB = os.path.join(HERE, "libmi_moe.so")
 SOURCES = ["route.hip", "sort.hip", "gemm1.hip", "gemm2.hip", "gemm1_tile.hip", "gemm2_tile.hip",
-           "gemm1_wide.hip", "gemm2_combine.hip", "combine.hip", "quant.hip", "capi.hip"]
+           "gemm1_wide.hip", "gemm2_wide.hip", "gemm2_combine.hip", "combine.hip", "quant.hip", "capi.hip"]
 PEAKS_LIB = os.path.join(HERE, "libmi_peaks.so")
 PEAKS_SOURCES = ["peaks.hip"]
 # Per-source flags: MFMA results in VGPRs rather than AGPRs.
@@ -29,7 +29,8 @@ PEAKS_SOURCES = ["peaks.hip"]
 #   v_accvgpr_read per result register (GEMM1 stream 1% faster at T=64).
 SOURCE_FLAGS = {"peaks.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"],
                 "gemm1.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"],
-                "gemm1_wide.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"]}
+                "gemm1_wide.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"],
+                "gemm2_wide.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"]}
 ARCH = "gfx950"
 
 HIPCC_FLAGS = [

@@ -75,13 +75,13 @@ Variants pick_variants(int64_t T) {
     Variants v;
     // Measured on MI355X: single-wave streaming workgroups while an expert
     // has at most a few row tiles, 64-column GEMM2 waves from T = 64, the
-    // wide GEMM1 (128 rows, register-ring weights) for tens to ~150 rows per
-    // expert, the LDS-tiled kernels once experts hold hundreds of rows.
+    // wide kernels (register-ring weights, LDS activations) for roughly 5 to
+    // 70 rows per expert (GEMM2 from ~10 to ~15), the LDS-tiled kernels beyond.
     if (T <= 4) v = {5, VARIANT_GEMM2_COMBINE};  // one launch fewer where launches dominate
     else if (T <= 32) v = {9, 5};
     else if (T <= 128) v = {5, 14};
-    else if (T <= 192) v = {1, 13};
-    else if (T <= 256) v = {15, 13};
+    else if (T <= 192) v = {15, 13};
+    else if (T <= 256) v = {15, 15};
     else if (T <= 1536) v = {15, 3};
     else v = {3, 3};
     const char* env = getenv("MI_MOE_VARIANT");

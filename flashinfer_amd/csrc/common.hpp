@@ -146,14 +146,15 @@ hipError_t launch_gemm2_tile(const Plan& p, const uint8_t* w2, const float* w2s,
                              hipStream_t s);
 hipError_t launch_gemm1_wide(const Plan& p, const uint8_t* hs, const float* hs_scale,
                              const uint8_t* w1, const float* w1s, hipStream_t s);
+hipError_t launch_gemm2_wide(const Plan& p, const uint8_t* w2, const float* w2s, hipStream_t s);
 
 // GEMM kernel variants: 0/1/2 weight-streaming with 16/32/64-row tiles and
 // 4-wave workgroups, 3 LDS-tiled large (GEMM1 256 rows, GEMM2 128 rows),
 // 4 LDS-tiled medium (GEMM1 128 rows, GEMM2 64 rows), 5..14 weight-streaming
 // shapes with 1-, 2-, 4- or 8-wave workgroups and 16/32/64 columns per wave
-// (see the launchers), 10 GEMM2 fused with the combine, 15 GEMM1 "wide"
-// tiles (128 rows; weights through a per-wave register ring, activations
-// through LDS) for medium row counts, with GEMM2 on the large LDS tile.
+// (see the launchers), 10 GEMM2 fused with the combine, 15 "wide" tiles
+// (64 rows for GEMM1, 32 for GEMM2; weights through a per-wave register
+// ring, activations through LDS) for medium row counts.
 constexpr int NUM_VARIANTS = 16;
 // GEMM2 variant that also performs the combine (decode sizes only).
 constexpr int VARIANT_GEMM2_COMBINE = 10;

@@ -128,7 +128,7 @@ int gemm1_bm(int variant) {
         case 4: return 128;
         case 11: return 32;
         case 12: return 32;
-        case 15: return 128;
+        case 15: return 64;
         default: return 16;
     }
 }

@@ -32,6 +32,7 @@ constexpr int lcm_c(int a, int b) { return a / gcd_c(a, b) * b; }
 
 constexpr int WIDE_NW = 4;                  // waves per workgroup
 constexpr int WIDE_G = 16 * WIDE_NW;        // gate columns per workgroup
+constexpr int WIDE_BM = 64;                 // rows per workgroup (see the launcher)
 
 template <int MTW, int D, int DA>
 __global__ __launch_bounds__(64 * WIDE_NW) void gemm1_wide_kernel(Plan p, const uint8_t* __restrict__ hs,
@@ -197,9 +198,12 @@ __global__ __launch_bounds__(64 * WIDE_NW) void gemm1_wide_kernel(Plan p, const 
 
 hipError_t launch_gemm1_wide(const Plan& p, const uint8_t* hs, const float* hs_scale,
                              const uint8_t* w1, const float* w1s, hipStream_t s) {
-    dim3 grid(I / WIDE_G, max_mtiles(p.T, 128));
-    hipLaunchKernelGGL((gemm1_wide_kernel<8, 4, 2>), grid, dim3(64 * WIDE_NW), 0, s, p, hs,
-                       hs_scale, w1, w1s);
+    // 64 rows, weights 2 k-blocks ahead, activations 1 ahead: 130 VGPRs, so
+    // three waves per SIMD. Measured against 32-, 96- and 128-row tiles and
+    // 4- to 8-deep rings, more resident waves beat deeper rings here.
+    dim3 grid(I / WIDE_G, max_mtiles(p.T, WIDE_BM));
+    hipLaunchKernelGGL((gemm1_wide_kernel<WIDE_BM / 16, 2, 1>), grid, dim3(64 * WIDE_NW), 0, s,
+                       p, hs, hs_scale, w1, w1s);
     return hipGetLastError();
 }
 

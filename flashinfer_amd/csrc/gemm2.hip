@@ -158,7 +158,7 @@ int gemm2_bm(int variant) {
         case 4: return 64;
         case 7: return 32;
         case 12: return 32;
-        case 15: return 128;  // the large LDS tile (GEMM2 has no wide kernel)
+        case 15: return 32;
         default: return 16;
     }
 }
@@ -173,7 +173,7 @@ hipError_t launch_gemm2(const Plan& p, const uint8_t* w2, const float* w2s, int 
                         hipStream_t s) {
     if (p.T <= 0) return hipSuccess;
     if (variant >= 3 && variant <= 4) return launch_gemm2_tile(p, w2, w2s, variant, s);
-    if (variant == 15) return launch_gemm2_tile(p, w2, w2s, 3, s);
+    if (variant == 15) return launch_gemm2_wide(p, w2, w2s, s);
     switch (variant) {
         case 0: launch_stream2<1, 4, 4, 2>(p, w2, w2s, s); break;
         case 1: launch_stream2<2, 4, 4, 2>(p, w2, w2s, s); break;
