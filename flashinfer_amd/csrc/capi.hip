@@ -73,13 +73,13 @@ bool fuse_front_end(int64_t T) {
 
 Variants pick_variants(int64_t T) {
     Variants v;
-    // Measured on MI355X: single-wave streaming workgroups while an expert
-    // has at most a few row tiles, 64-column GEMM2 waves from T = 64, the
+    // Measured on MI355X: streaming workgroups (GEMM1 with K split over 4
+    // waves) while an expert has at most a few row tiles, 64-column GEMM2 waves from T = 64, the
     // wide kernels (register-ring weights, LDS activations) for roughly 5 to
     // 70 rows per expert (GEMM2 from ~10 to ~15), the LDS-tiled kernels beyond.
     if (T <= 4) v = {5, VARIANT_GEMM2_COMBINE};  // one launch fewer where launches dominate
-    else if (T <= 32) v = {9, 5};
-    else if (T <= 128) v = {5, 14};
+    else if (T <= 32) v = {16, 5};
+    else if (T <= 128) v = {16, 14};
     else if (T <= 192) v = {15, 13};
     else if (T <= 256) v = {15, 15};
     else if (T <= 1536) v = {15, 3};

@@ -154,8 +154,10 @@ hipError_t launch_gemm2_wide(const Plan& p, const uint8_t* w2, const float* w2s,
 // shapes with 1-, 2-, 4- or 8-wave workgroups and 16/32/64 columns per wave
 // (see the launchers), 10 GEMM2 fused with the combine, 15 "wide" tiles
 // (64 rows for GEMM1, 32 for GEMM2; weights through a per-wave register
-// ring, activations through LDS) for medium row counts.
-constexpr int NUM_VARIANTS = 16;
+// ring, activations through LDS) for medium row counts, 16 GEMM1 streaming
+// with K split over 4 waves of a workgroup. An id without a kernel of its own
+// in one GEMM (9 and 16 for GEMM2) runs that GEMM's default stream shape.
+constexpr int NUM_VARIANTS = 17;
 // GEMM2 variant that also performs the combine (decode sizes only).
 constexpr int VARIANT_GEMM2_COMBINE = 10;
 

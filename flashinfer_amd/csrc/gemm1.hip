@@ -9,11 +9,14 @@
 // 128-wide scale block, so the product of the two block scales is applied
 // to each MFMA result in the fp32 accumulator (kernel.py:168-171).
 //
-// "Stream" variant (template <MT, D, NW>): weight tiles are not reused across
-// row tiles, so they go global -> VGPR with a D-deep register prefetch ring
-// instead of through LDS. A workgroup is NW waves; wave w owns gate columns
-// j0..j0+15 and the matching up columns I+j0..I+j0+15 for the BM = 16*MT rows
-// of one expert's row tile.
+// "Stream" variant (template <MT, D, NW, KS>): weight tiles are not reused
+// across row tiles, so they go global -> VGPR with a D-deep register prefetch
+// ring instead of through LDS. A workgroup is NW * KS waves; wave w owns gate
+// columns j0..j0+15 and the matching up columns I+j0..I+j0+15 of column group
+// w % NW for the BM = 16*MT rows of one expert's row tile, over k-blocks
+// [(w / NW) * 56/KS, +56/KS): with KS > 1 the waves of a column group split K
+// and add their partial sums through LDS in a fixed order, which gives few
+// active experts more waves in flight.
 //
 // Operand layout: lane l feeds row (l % 16) of a 16x128 operand with bytes
 // [16g, 16g+16) and [64+16g, 64+16g+16) of the 128-byte k-block, g = l / 16.
@@ -23,14 +26,17 @@
 
 namespace mimoe {
 
-template <int MT, int D, int NW>
-__global__ __launch_bounds__(64 * NW) void gemm1_stream_kernel(Plan p, const uint8_t* __restrict__ hs,
-                                                               const float* __restrict__ hs_scale,
-                                                               const uint8_t* __restrict__ w1,
-                                                               const float* __restrict__ w1s) {
-    static_assert(HB % D == 0, "prefetch depth must divide the k-block count");
+template <int MT, int D, int NW, int KS = 1>
+__global__ __launch_bounds__(64 * NW * KS) void gemm1_stream_kernel(Plan p, const uint8_t* __restrict__ hs,
+                                                                    const float* __restrict__ hs_scale,
+                                                                    const uint8_t* __restrict__ w1,
+                                                                    const float* __restrict__ w1s) {
+    constexpr int KB = HB / KS;  // k-blocks per wave
+    static_assert(HB % KS == 0 && KB % D == 0, "k split and prefetch depth must divide the k-blocks");
     constexpr int BM = 16 * MT;
     __shared__ float sa_lds[HB][BM];
+    // partial sums of waves 1..KS-1 of a column group: [split-1][group][value][lane]
+    __shared__ float red[KS > 1 ? KS - 1 : 1][NW][KS > 1 ? 8 * MT : 1][64];
 
     int e, row0, nrows;
     if (!find_tile(p.meta, META_MTILE1, blockIdx.y, BM, e, row0, nrows)) return;
@@ -38,16 +44,19 @@ __global__ __launch_bounds__(64 * NW) void gemm1_stream_kernel(Plan p, const uin
     const int tid = threadIdx.x;
     const int lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const int j0 = blockIdx.x * (16 * NW) + wave * 16;
+    const int wc = wave % NW;         // column group
+    const int ks = wave / NW;         // k split: k-blocks [ks*KB, ks*KB + KB)
+    const int j0 = blockIdx.x * (16 * NW) + wc * 16;
     const int r = lane & 15, g = lane >> 4;
-    const uint8_t* bg_ptr = w1 + ((size_t)e * N1 + j0 + r) * H + g * 16;
-    const uint8_t* bu_ptr = w1 + ((size_t)e * N1 + I + j0 + r) * H + g * 16;
+    const uint8_t* bg_ptr = w1 + ((size_t)e * N1 + j0 + r) * H + (size_t)ks * KB * BLK + g * 16;
+    const uint8_t* bu_ptr = w1 + ((size_t)e * N1 + I + j0 + r) * H + (size_t)ks * KB * BLK + g * 16;
     const uint8_t* a_ptr[MT];
 #pragma unroll
     for (int i = 0; i < MT; ++i)
-        a_ptr[i] = hs + (size_t)p.sorted_tok[row0 + min(i * 16 + r, nrows - 1)] * H + g * 16;
-    const float* sbg_ptr = w1s + ((size_t)e * N1B + j0 / BLK) * HB;
-    const float* sbu_ptr = w1s + ((size_t)e * N1B + (I + j0) / BLK) * HB;
+        a_ptr[i] = hs + (size_t)p.sorted_tok[row0 + min(i * 16 + r, nrows - 1)] * H + ks * KB * BLK + g * 16;
+    const float* sbg_ptr = w1s + ((size_t)e * N1B + j0 / BLK) * HB + ks * KB;
+    const float* sbu_ptr = w1s + ((size_t)e * N1B + (I + j0) / BLK) * HB + ks * KB;
+    const float (*sa_k)[BM] = sa_lds + ks * KB;  // this wave's k-blocks
 
     v8i bg[D], bu[D], a[D][MT];
     v4f accg[MT], accu[MT];
@@ -64,7 +73,7 @@ __global__ __launch_bounds__(64 * NW) void gemm1_stream_kernel(Plan p, const uin
         for (int i = 0; i < MT; ++i) {
             const v4f pg = mfma_f8_16x16x128(a[d][i], bg[d], zero);
             const v4f pu = mfma_f8_16x16x128(a[d][i], bu[d], zero);
-            const float4 sa4 = *reinterpret_cast<const float4*>(&sa_lds[kb][i * 16 + g * 4]);
+            const float4 sa4 = *reinterpret_cast<const float4*>(&sa_k[kb][i * 16 + g * 4]);
             accg[i][0] += pg[0] * (sa4.x * sg);
             accg[i][1] += pg[1] * (sa4.y * sg);
             accg[i][2] += pg[2] * (sa4.z * sg);
@@ -87,7 +96,7 @@ __global__ __launch_bounds__(64 * NW) void gemm1_stream_kernel(Plan p, const uin
     // LDS while those loads are in flight.
 #pragma unroll
     for (int d = 0; d < D; ++d) load(d, d);
-    for (int i = tid; i < HB * BM; i += 64 * NW) {
+    for (int i = tid; i < HB * BM; i += 64 * NW * KS) {
         const int kb = i / BM, m = i % BM;
         sa_lds[kb][m] = hs_scale[(size_t)kb * p.T + p.sorted_tok[row0 + min(m, nrows - 1)]];
     }
@@ -95,7 +104,7 @@ __global__ __launch_bounds__(64 * NW) void gemm1_stream_kernel(Plan p, const uin
 
     // Steady state: every stage is refilled right after it is consumed.
 #pragma unroll 1
-    for (int kb0 = 0; kb0 < HB - D; kb0 += D) {
+    for (int kb0 = 0; kb0 < KB - D; kb0 += D) {
 #pragma unroll
         for (int d = 0; d < D; ++d) {
             compute(d, kb0 + d);
@@ -104,7 +113,32 @@ __global__ __launch_bounds__(64 * NW) void gemm1_stream_kernel(Plan p, const uin
     }
     // Drain the last D k-blocks.
 #pragma unroll
-    for (int d = 0; d < D; ++d) compute(d, HB - D + d);
+    for (int d = 0; d < D; ++d) compute(d, KB - D + d);
+
+    // K split: the other waves of the column group hand their partial sums to
+    // the first through LDS, which adds them in split order (deterministic).
+    if constexpr (KS > 1) {
+        if (ks > 0) {
+#pragma unroll
+            for (int i = 0; i < MT; ++i)
+#pragma unroll
+                for (int rr = 0; rr < 4; ++rr) {
+                    red[ks - 1][wc][8 * i + rr][lane] = accg[i][rr];
+                    red[ks - 1][wc][8 * i + 4 + rr][lane] = accu[i][rr];
+                }
+        }
+        __syncthreads();
+        if (ks > 0) return;
+#pragma unroll
+        for (int k = 0; k < KS - 1; ++k)
+#pragma unroll
+            for (int i = 0; i < MT; ++i)
+#pragma unroll
+                for (int rr = 0; rr < 4; ++rr) {
+                    accg[i][rr] += red[k][wc][8 * i + rr][lane];
+                    accu[i][rr] += red[k][wc][8 * i + 4 + rr][lane];
+                }
+    }
 
 #pragma unroll
     for (int i = 0; i < MT; ++i) {
@@ -133,11 +167,11 @@ int gemm1_bm(int variant) {
     }
 }
 
-template <int MT, int D, int NW>
+template <int MT, int D, int NW, int KS = 1>
 static void launch_stream1(const Plan& p, const uint8_t* hs, const float* hs_scale,
                            const uint8_t* w1, const float* w1s, hipStream_t s) {
     dim3 grid(I / (16 * NW), max_mtiles(p.T, 16 * MT));
-    hipLaunchKernelGGL((gemm1_stream_kernel<MT, D, NW>), grid, dim3(64 * NW), 0, s, p, hs,
+    hipLaunchKernelGGL((gemm1_stream_kernel<MT, D, NW, KS>), grid, dim3(64 * NW * KS), 0, s, p, hs,
                        hs_scale, w1, w1s);
 }
 
@@ -156,6 +190,7 @@ hipError_t launch_gemm1(const Plan& p, const uint8_t* hs, const float* hs_scale,
         case 8: launch_stream1<1, 4, 2>(p, hs, hs_scale, w1, w1s, s); break;
         case 11: launch_stream1<2, 4, 1>(p, hs, hs_scale, w1, w1s, s); break;
         case 12: launch_stream1<2, 2, 1>(p, hs, hs_scale, w1, w1s, s); break;
+        case 16: launch_stream1<1, 2, 1, 4>(p, hs, hs_scale, w1, w1s, s); break;
         default: launch_stream1<1, 2, 1>(p, hs, hs_scale, w1, w1s, s); break;
     }
     return hipGetLastError();
