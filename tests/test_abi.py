@@ -141,3 +141,21 @@ def test_python_wrapper_validates_shapes_and_device():
         kernel.run(**bad)
     with pytest.raises(ValueError, match="GPU"):
         kernel.run(**good)
+
+
+def test_phase_timing_switch(monkeypatch):
+    """Timing is on only with FIB_PROFILE_PHASES=1 and an output path, and only
+    until the first file is written (kernel.py:30-35 of the reference)."""
+    monkeypatch.setattr(kernel, "_PHASE_TIMING_EMITTED", False)
+    monkeypatch.delenv("FIB_PROFILE_PHASES", raising=False)
+    monkeypatch.delenv("FIB_PHASE_TIMING_OUTPUT", raising=False)
+    assert not kernel._phase_timing_enabled()
+    monkeypatch.setenv("FIB_PROFILE_PHASES", "1")
+    assert not kernel._phase_timing_enabled()
+    monkeypatch.setenv("FIB_PHASE_TIMING_OUTPUT", "/tmp/x.json")
+    assert kernel._phase_timing_enabled()
+    monkeypatch.setenv("FIB_PROFILE_PHASES", "0")
+    assert not kernel._phase_timing_enabled()
+    monkeypatch.setenv("FIB_PROFILE_PHASES", "1")
+    monkeypatch.setattr(kernel, "_PHASE_TIMING_EMITTED", True)
+    assert not kernel._phase_timing_enabled()
