@@ -25,8 +25,8 @@ MI_MOE_DTYPE_BF16 = 0
 MI_MOE_DTYPE_F32 = 1
 
 EXPORTED = ("mi_moe_workspace_size", "mi_moe_workspace_layout", "mi_moe_run",
-            "mi_moe_run_profiled", "mi_moe_route", "mi_moe_quantize_fp8", "mi_moe_last_error",
-            "mi_moe_version")
+            "mi_moe_run_profiled", "mi_moe_route", "mi_moe_sort", "mi_moe_quantize_fp8",
+            "mi_moe_last_error", "mi_moe_version")
 NUM_PHASES = 5
 PHASES = ("route", "sort", "gemm1_swiglu", "gemm2", "combine")
 
@@ -92,6 +92,9 @@ def lib() -> ctypes.CDLL:
         L.mi_moe_route.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int32, ctypes.c_int64,
                                    ctypes.c_float, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p]
         L.mi_moe_route.restype = ctypes.c_int
+        L.mi_moe_sort.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int64, ctypes.c_int64,
+                                  ctypes.c_void_p, ctypes.c_size_t, ctypes.c_void_p]
+        L.mi_moe_sort.restype = ctypes.c_int
         L.mi_moe_quantize_fp8.argtypes = [ctypes.c_void_p, ctypes.c_int64, ctypes.c_void_p,
                                           ctypes.c_void_p, ctypes.c_void_p]
         L.mi_moe_quantize_fp8.restype = ctypes.c_int

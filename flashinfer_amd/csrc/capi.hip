@@ -57,6 +57,30 @@ mi_moe_layout make_layout(int64_t T) {
 
 bool aligned(const void* p, size_t a) { return ((uintptr_t)p % a) == 0; }
 
+// Device pointers of one call into the caller's workspace.
+Plan make_plan(void* workspace, const mi_moe_layout& L, int64_t T, int64_t local_expert_offset,
+               float rsf) {
+    // Offsets outside [-2^30, 2^30] select no expert; clamp so int math stays exact.
+    int64_t off = local_expert_offset;
+    if (off > (1 << 30)) off = 1 << 30;
+    if (off < -(1 << 30)) off = -(1 << 30);
+    uint8_t* ws = (uint8_t*)workspace;
+    Plan p;
+    p.T = (int)T;
+    p.local_offset = (int)off;
+    p.rsf = rsf;
+    p.topk_ids = (int*)(ws + L.topk_ids);
+    p.topk_w = (float*)(ws + L.topk_w);
+    p.meta = (int*)(ws + L.expert_off);
+    p.sorted_tok = (int*)(ws + L.sorted_tok);
+    p.sorted_w = (float*)(ws + L.sorted_w);
+    p.tok_slot = (int*)(ws + L.tok_slot);
+    p.chunk_cnt = (int*)(ws + L.chunk_cnt);
+    p.act = (uint16_t*)(ws + L.act);
+    p.part = (uint16_t*)(ws + L.part);
+    return p;
+}
+
 // GEMM variants by token count. MI_MOE_VARIANT="v" or "v1,v2" overrides
 // (0..NUM_VARIANTS-1, for tests and tuning).
 struct Variants {
@@ -139,6 +163,31 @@ int mi_moe_route(const float* routing_logits, const void* routing_bias, int32_t 
     return MI_MOE_OK;
 }
 
+int mi_moe_sort(const int32_t* topk_ids, const float* topk_weights, int64_t num_tokens,
+                int64_t local_expert_offset, void* workspace, size_t workspace_bytes, void* stream) {
+    g_last_error.clear();
+    if (num_tokens < 0 || num_tokens > kMaxTokens)
+        return fail(MI_MOE_ERR_INVALID, "mi_moe_sort: num_tokens %lld out of range",
+                    (long long)num_tokens);
+    if (num_tokens == 0) return MI_MOE_OK;
+    if (!topk_ids || !topk_weights || !workspace)
+        return fail(MI_MOE_ERR_INVALID, "mi_moe_sort: NULL pointer argument");
+    if (!aligned(topk_ids, 16) || !aligned(topk_weights, 16) || !aligned(workspace, 256))
+        return fail(MI_MOE_ERR_INVALID, "mi_moe_sort: misaligned pointer");
+    const mi_moe_layout L = make_layout(num_tokens);
+    if (workspace_bytes < L.total)
+        return fail(MI_MOE_ERR_WORKSPACE, "mi_moe_sort: workspace has %zu bytes, needs %zu",
+                    workspace_bytes, L.total);
+    Plan p = make_plan(workspace, L, num_tokens, local_expert_offset, 0.f);
+    p.topk_ids = const_cast<int*>(topk_ids);  // read only
+    p.topk_w = const_cast<float*>(topk_weights);
+    const Variants var = pick_variants(num_tokens);
+    hipError_t err = launch_sort(p, gemm1_bm(var.g1), gemm2_bm(var.g2), (hipStream_t)stream);
+    if (err != hipSuccess)
+        return fail(MI_MOE_ERR_HIP, "mi_moe_sort: launch failed: %s", hipGetErrorString(err));
+    return MI_MOE_OK;
+}
+
 int mi_moe_quantize_fp8(const void* hidden_bf16, int64_t num_tokens, uint8_t* hidden_states,
                         float* hidden_states_scale, void* stream) {
     g_last_error.clear();
@@ -201,25 +250,7 @@ static int run_impl(const mi_moe_args* a, hipStream_t s, hipEvent_t const* ev) {
         return fail(MI_MOE_ERR_WORKSPACE, "mi_moe_run: workspace has %zu bytes, needs %zu",
                     a->workspace_bytes, L.total);
 
-    // Offsets outside [-2^30, 2^30] select no expert; clamp so int math stays exact.
-    int64_t off = a->local_expert_offset;
-    if (off > (1 << 30)) off = 1 << 30;
-    if (off < -(1 << 30)) off = -(1 << 30);
-
-    uint8_t* ws = (uint8_t*)a->workspace;
-    Plan p;
-    p.T = (int)T;
-    p.local_offset = (int)off;
-    p.rsf = a->routed_scaling_factor;
-    p.topk_ids = (int*)(ws + L.topk_ids);
-    p.topk_w = (float*)(ws + L.topk_w);
-    p.meta = (int*)(ws + L.expert_off);
-    p.sorted_tok = (int*)(ws + L.sorted_tok);
-    p.sorted_w = (float*)(ws + L.sorted_w);
-    p.tok_slot = (int*)(ws + L.tok_slot);
-    p.chunk_cnt = (int*)(ws + L.chunk_cnt);
-    p.act = (uint16_t*)(ws + L.act);
-    p.part = (uint16_t*)(ws + L.part);
+    Plan p = make_plan(a->workspace, L, T, a->local_expert_offset, a->routed_scaling_factor);
 
     const Variants var = pick_variants(T);
     hipError_t err = hipSuccess;

@@ -230,6 +230,43 @@ def route(routing_logits: torch.Tensor, routing_bias: torch.Tensor, routed_scali
     return ids, w
 
 
+def sort(topk_ids: torch.Tensor, topk_weights: torch.Tensor, local_expert_offset: int):
+    """Local-expert sort only (kernel.py:460-516), for staged checks: from global
+    top-8 ids int32 [T,8] and weights fp32 [T,8] (those of ``route``, or any
+    others), the tables ``run``'s sort builds. Returns ``(expert_offsets int32
+    [33], sorted_token_ids int32 [S], sorted_weights fp32 [S], token_slots int32
+    [T,8])``; slots are grouped by local expert, token-ascending inside one,
+    and a token's slots are listed by ascending local expert, then -1. Reading
+    S back synchronises the stream (a debugging entry point, not the hot path)."""
+    if not isinstance(topk_ids, torch.Tensor) or topk_ids.dim() != 2:
+        raise ValueError("topk_ids must be a 2-D tensor [T, 8]")
+    T = int(topk_ids.shape[0])
+    _expect(topk_ids, "topk_ids", (torch.int32,), (T, 8))
+    _expect(topk_weights, "topk_weights", (torch.float32,), (T, 8))
+    dev = topk_ids.device
+    if dev.type != "cuda" or topk_weights.device != dev:
+        raise ValueError("sort() needs both tensors on the same ROCm GPU")
+    offset = _scalar(local_expert_offset, int)
+    if T == 0:
+        empty = torch.empty(0, dtype=torch.int32, device=dev)
+        return (torch.zeros(E_LOCAL + 1, dtype=torch.int32, device=dev), empty,
+                torch.empty(0, dtype=torch.float32, device=dev),
+                torch.empty(0, 8, dtype=torch.int32, device=dev))
+    ids, w = topk_ids.contiguous(), topk_weights.contiguous()
+    with torch.cuda.device(dev):
+        stream = torch.cuda.current_stream(dev).cuda_stream
+        ws = _workspace(dev, stream, _lib.workspace_size(T))
+        _lib.check(_lib.lib().mi_moe_sort(ids.data_ptr(), w.data_ptr(), T, offset, ws.data_ptr(),
+                                          ws.numel(), ctypes.c_void_p(stream)))
+        L = _lib.workspace_layout(T)
+        eoff = ws[L.expert_off:L.expert_off + (E_LOCAL + 1) * 4].view(torch.int32).clone()
+        S = int(eoff[E_LOCAL].item())
+        stok = ws[L.sorted_tok:L.sorted_tok + S * 4].view(torch.int32).clone()
+        sw = ws[L.sorted_w:L.sorted_w + S * 4].view(torch.float32).clone()
+        slots = ws[L.tok_slot:L.tok_slot + T * 32].view(torch.int32).view(T, 8).clone()
+    return eoff, stok, sw, slots
+
+
 def quantize_activations(hidden: torch.Tensor, hidden_states: torch.Tensor | None = None,
                          hidden_states_scale: torch.Tensor | None = None):
     """FP8 activation quantiser feeding ``run``: bf16 ``hidden`` [T, 7168] ->

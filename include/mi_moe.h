@@ -99,6 +99,19 @@ int mi_moe_route(const float* routing_logits, const void* routing_bias, int32_t 
                  int64_t num_tokens, float routed_scaling_factor, int32_t* topk_ids,
                  float* topk_weights, void* stream);
 
+/* Local-expert sort only (kernel.py:460-516 and the scan at :572-581), for
+ * staged parity: from global top-8 ids (int32 [T, 8]) and weights (fp32
+ * [T, 8]), e.g. those of mi_moe_route, writes into the workspace (offsets from
+ * mi_moe_workspace_layout) what mi_moe_run's sort writes: expert_off int32[33]
+ * (followed by the row-tile prefixes of T's default GEMM kernels),
+ * sorted_tok / sorted_w [S] (slots grouped by local expert, token-ascending
+ * inside an expert) and tok_slot int32 [T, 8] (a token's slots in ascending
+ * local expert, then -1). Ids outside [local_expert_offset,
+ * local_expert_offset + 32) are not local. topk pointers 16-byte aligned,
+ * workspace 256-byte aligned and at least mi_moe_workspace_size(T) bytes. */
+int mi_moe_sort(const int32_t* topk_ids, const float* topk_weights, int64_t num_tokens,
+                int64_t local_expert_offset, void* workspace, size_t workspace_bytes, void* stream);
+
 /* FP8 activation quantiser feeding mi_moe_run: bf16 hidden states [T, 7168]
  * -> hidden_states fp8 e4m3fn [T, 7168] and hidden_states_scale fp32 [56, T]
  * (block-major, the layout kernel.py:169 reads). Per token and 128-element

@@ -112,6 +112,20 @@ def test_route_rejects_before_launch():
     assert L.mi_moe_route(None, None, 0, 0, 2.5, None, None, None) == _lib.MI_MOE_OK
 
 
+def test_sort_rejects_before_launch():
+    L = _lib.lib()
+    fake = 1 << 20  # never dereferenced: every check runs before a launch
+    ws = _lib.workspace_size(16)
+    assert L.mi_moe_sort(None, None, -1, 0, None, 0, None) == _lib.MI_MOE_ERR_INVALID
+    assert L.mi_moe_sort(None, None, 1 << 23, 0, None, 0, None) == _lib.MI_MOE_ERR_INVALID
+    assert L.mi_moe_sort(None, None, 16, 0, fake, ws, None) == _lib.MI_MOE_ERR_INVALID
+    assert L.mi_moe_sort(fake + 4, fake, 16, 0, fake, ws, None) == _lib.MI_MOE_ERR_INVALID
+    assert L.mi_moe_sort(fake, fake, 16, 0, fake + 16, ws, None) == _lib.MI_MOE_ERR_INVALID
+    assert L.mi_moe_sort(fake, fake, 16, 0, fake, ws - 1, None) == _lib.MI_MOE_ERR_WORKSPACE
+    assert "workspace" in L.mi_moe_last_error().decode()
+    assert L.mi_moe_sort(None, None, 0, 0, None, 0, None) == _lib.MI_MOE_OK
+
+
 def test_quantize_rejects_before_launch():
     L = _lib.lib()
     assert L.mi_moe_quantize_fp8(None, -1, None, None, None) == _lib.MI_MOE_ERR_INVALID

@@ -275,3 +275,59 @@ def test_front_end_fused_and_split_agree(name, fuse, monkeypatch):
     wl = W.standard(name)
     out = run_gpu(wl, fill=float("nan"))
     _check_output(wl, out, spread_tokens(wl.T, 64))
+
+
+def _check_sort_tables(ids, w, offset, got):
+    """The sort entry point's tables against the oracle's local assignment."""
+    from oracle import ref_moe as R
+    eoff, stok, sw, slots = [x.cpu() for x in got]
+    T = ids.shape[0]
+    want = R.local_assignment(ids.long(), w, offset, 32)
+    counts = torch.tensor([len(tk) for tk, _ in want])
+    want_off = torch.cat([torch.zeros(1, dtype=torch.long), counts.cumsum(0)])
+    assert torch.equal(eoff.long(), want_off)
+    assert torch.equal(stok.long(), torch.cat([tk for tk, _ in want]))
+    assert torch.equal(sw, torch.cat([x for _, x in want]).float())
+    # token -> slots: ascending local expert, then -1
+    expect = torch.full((T, 8), -1, dtype=torch.long)
+    fill = torch.zeros(T, dtype=torch.long)
+    for e, (tk, _) in enumerate(want):
+        pos = int(want_off[e]) + torch.arange(len(tk))
+        expect[tk, fill[tk]] = pos
+        fill[tk] += 1
+    assert torch.equal(slots.long(), expect)
+
+
+@pytest.mark.parametrize("name", ["c1_t4", "c1_t64", "c2_t1024_o128", "c3_t8192"])
+def test_sort_entry_from_oracle_routing(name):
+    """mi_moe_sort fed with the oracle's routing (not the GPU's) builds exactly
+    the oracle's local assignment: one-wave, one-workgroup and chunked sorts."""
+    from flashinfer_amd import kernel
+    from oracle import ref_moe as R
+    log(f"test_sort_entry_from_oracle_routing[{name}]")
+    wl = W.standard(name)
+    r = R.route(wl.tensors["routing_logits"], wl.tensors["routing_bias"], wl.routed_scaling_factor)
+    ids = r.ids.to(torch.int32)
+    w = r.weights.to(torch.float32)
+    got = kernel.sort(ids.cuda(), w.cuda(), wl.local_expert_offset)
+    _check_sort_tables(ids, w, wl.local_expert_offset, got)
+
+
+@pytest.mark.parametrize("T,offset,mode", [(2049, 0, "same8"), (3000, 96, "random"), (64, 224, "none"),
+                                           (1, 0, "same8"), (1024, 32, "random")])
+def test_sort_entry_adversarial(T, offset, mode):
+    """Every token on the same 8 local experts (one expert holds T slots, across
+    sort chunks), random distinct ids over all 256 experts, and no local id."""
+    from flashinfer_amd import kernel
+    log(f"test_sort_entry_adversarial[T={T}-{mode}]")
+    g = torch.Generator().manual_seed(T + offset)
+    if mode == "same8":
+        ids = (offset + torch.tensor([3, 0, 7, 1, 30, 12, 5, 31])).repeat(T, 1)
+    elif mode == "random":
+        ids = torch.stack([torch.randperm(256, generator=g)[:8] for _ in range(T)])
+    else:
+        ids = torch.randint(0, offset, (T, 8), generator=g)
+    ids = ids.to(torch.int32)
+    w = torch.rand(T, 8, generator=g)
+    got = kernel.sort(ids.cuda(), w.cuda(), offset)
+    _check_sort_tables(ids, w, offset, got)
