@@ -1,4 +1,5 @@
-"""ctypes binding of libmi_moe.so (the C ABI in include/mi_moe.h).
+"""ctypes binding of libmi_moe.so (the C ABI in include/mi_moe.h), and of
+the libraries built for other (H, I) shapes (``shapes.py``), one per shape.
 
 The library is loaded after ``import torch`` so that its ``libamdhip64.so.7``
 dependency binds to the HIP runtime torch already loaded (same SONAME):
@@ -14,8 +15,11 @@ import threading
 
 import torch  # noqa: F401  (must precede the CDLL load, see module docstring)
 
+from . import shapes
+
 HERE = os.path.dirname(os.path.abspath(__file__))
-LIB_PATH = os.path.join(HERE, "libmi_moe.so")
+LIB_PATH = os.path.join(HERE, "libmi_moe.so")  # the default shape (H=7168, I=2048)
+DEFAULT_SHAPE = shapes.DEFAULT_SHAPE
 
 MI_MOE_OK = 0
 MI_MOE_ERR_INVALID = 1
@@ -26,7 +30,7 @@ MI_MOE_DTYPE_F32 = 1
 
 EXPORTED = ("mi_moe_workspace_size", "mi_moe_workspace_layout", "mi_moe_run",
             "mi_moe_run_profiled", "mi_moe_route", "mi_moe_sort", "mi_moe_quantize_fp8",
-            "mi_moe_last_error", "mi_moe_version")
+            "mi_moe_shape", "mi_moe_last_error", "mi_moe_version")
 NUM_PHASES = 5
 PHASES = ("route", "sort", "gemm1_swiglu", "gemm2", "combine")
 
@@ -58,7 +62,7 @@ class MiMoeLayout(ctypes.Structure):
                  "chunk_cnt", "act", "part", "total")]
 
 
-_lib = None
+_libs: dict = {}
 _lock = threading.Lock()
 
 
@@ -68,55 +72,85 @@ class MiMoeError(RuntimeError):
         self.code = code
 
 
-def lib() -> ctypes.CDLL:
-    global _lib
-    if _lib is not None:
-        return _lib
+def _bind(L: ctypes.CDLL) -> None:
+    L.mi_moe_workspace_size.argtypes = [ctypes.c_int64]
+    L.mi_moe_workspace_size.restype = ctypes.c_size_t
+    L.mi_moe_workspace_layout.argtypes = [ctypes.c_int64, ctypes.POINTER(MiMoeLayout)]
+    L.mi_moe_workspace_layout.restype = ctypes.c_int
+    L.mi_moe_run.argtypes = [ctypes.POINTER(MiMoeArgs), ctypes.c_void_p]
+    L.mi_moe_run.restype = ctypes.c_int
+    L.mi_moe_run_profiled.argtypes = [ctypes.POINTER(MiMoeArgs), ctypes.c_void_p,
+                                      ctypes.POINTER(ctypes.c_void_p), ctypes.c_int32]
+    L.mi_moe_run_profiled.restype = ctypes.c_int
+    L.mi_moe_route.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int32, ctypes.c_int64,
+                               ctypes.c_float, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p]
+    L.mi_moe_route.restype = ctypes.c_int
+    L.mi_moe_sort.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int64, ctypes.c_int64,
+                              ctypes.c_void_p, ctypes.c_size_t, ctypes.c_void_p]
+    L.mi_moe_sort.restype = ctypes.c_int
+    L.mi_moe_quantize_fp8.argtypes = [ctypes.c_void_p, ctypes.c_int64, ctypes.c_void_p,
+                                      ctypes.c_void_p, ctypes.c_void_p]
+    L.mi_moe_quantize_fp8.restype = ctypes.c_int
+    L.mi_moe_last_error.argtypes = []
+    L.mi_moe_last_error.restype = ctypes.c_char_p
+    L.mi_moe_version.argtypes = []
+    L.mi_moe_version.restype = ctypes.c_char_p
+    L.mi_moe_shape.argtypes = [ctypes.POINTER(ctypes.c_int32), ctypes.POINTER(ctypes.c_int32)]
+    L.mi_moe_shape.restype = ctypes.c_int
+
+
+def lib_path(shape=DEFAULT_SHAPE) -> str:
+    shape = (int(shape[0]), int(shape[1]))
+    return LIB_PATH if shape == DEFAULT_SHAPE else os.path.join(HERE, shapes.lib_name(*shape))
+
+
+def built_shapes() -> list:
+    """(H, I) of every library present next to this file."""
+    return [sh for sh in shapes.SHAPES if os.path.exists(lib_path(sh))]
+
+
+def lib(shape=DEFAULT_SHAPE) -> ctypes.CDLL:
+    """The library compiled for ``shape`` = (H, I), loaded once."""
+    shape = (int(shape[0]), int(shape[1]))
+    L = _libs.get(shape)
+    if L is not None:
+        return L
     with _lock:
-        if _lib is not None:
-            return _lib
-        if not os.path.exists(LIB_PATH):
-            raise RuntimeError(
-                f"{LIB_PATH} is missing: build it with `python -m flashinfer_amd.build` "
-                "(hipcc, gfx950). There is no non-native fallback.")
-        L = ctypes.CDLL(LIB_PATH)
-        L.mi_moe_workspace_size.argtypes = [ctypes.c_int64]
-        L.mi_moe_workspace_size.restype = ctypes.c_size_t
-        L.mi_moe_workspace_layout.argtypes = [ctypes.c_int64, ctypes.POINTER(MiMoeLayout)]
-        L.mi_moe_workspace_layout.restype = ctypes.c_int
-        L.mi_moe_run.argtypes = [ctypes.POINTER(MiMoeArgs), ctypes.c_void_p]
-        L.mi_moe_run.restype = ctypes.c_int
-        L.mi_moe_run_profiled.argtypes = [ctypes.POINTER(MiMoeArgs), ctypes.c_void_p,
-                                          ctypes.POINTER(ctypes.c_void_p), ctypes.c_int32]
-        L.mi_moe_run_profiled.restype = ctypes.c_int
-        L.mi_moe_route.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int32, ctypes.c_int64,
-                                   ctypes.c_float, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p]
-        L.mi_moe_route.restype = ctypes.c_int
-        L.mi_moe_sort.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int64, ctypes.c_int64,
-                                  ctypes.c_void_p, ctypes.c_size_t, ctypes.c_void_p]
-        L.mi_moe_sort.restype = ctypes.c_int
-        L.mi_moe_quantize_fp8.argtypes = [ctypes.c_void_p, ctypes.c_int64, ctypes.c_void_p,
-                                          ctypes.c_void_p, ctypes.c_void_p]
-        L.mi_moe_quantize_fp8.restype = ctypes.c_int
-        L.mi_moe_last_error.argtypes = []
-        L.mi_moe_last_error.restype = ctypes.c_char_p
-        L.mi_moe_version.argtypes = []
-        L.mi_moe_version.restype = ctypes.c_char_p
-        _lib = L
+        if shape in _libs:
+            return _libs[shape]
+        path = lib_path(shape)
+        if not os.path.exists(path):
+            if shape == DEFAULT_SHAPE:
+                raise RuntimeError(
+                    f"{path} is missing: build it with `python -m flashinfer_amd.build` "
+                    "(hipcc, gfx950). There is no non-native fallback.")
+            hint = ("add it to SHAPES in flashinfer_amd/shapes.py and rebuild"
+                    if shapes.supported(*shape) else
+                    "supported shapes have H % 1024 == 0 and I % 256 == 0")
+            raise ValueError(f"no library for hidden size {shape[0]} and intermediate size "
+                             f"{shape[1]} (built: {built_shapes()}); {hint}")
+        L = ctypes.CDLL(path)
+        _bind(L)
+        h, i = ctypes.c_int32(), ctypes.c_int32()
+        if L.mi_moe_shape(ctypes.byref(h), ctypes.byref(i)) != MI_MOE_OK or (h.value, i.value) != shape:
+            raise RuntimeError(f"{path} reports shape ({h.value}, {i.value}), expected {shape}")
+        _libs[shape] = L
         return L
 
 
-def check(code: int) -> None:
+def check(code: int, L: ctypes.CDLL | None = None) -> None:
+    """Raise with the library's message (each library keeps its own) on error."""
     if code != MI_MOE_OK:
-        msg = lib().mi_moe_last_error().decode("utf-8", "replace")
+        msg = (L or lib()).mi_moe_last_error().decode("utf-8", "replace")
         raise MiMoeError(code, msg)
 
 
-def workspace_size(num_tokens: int) -> int:
-    return int(lib().mi_moe_workspace_size(int(num_tokens)))
+def workspace_size(num_tokens: int, shape=DEFAULT_SHAPE) -> int:
+    return int(lib(shape).mi_moe_workspace_size(int(num_tokens)))
 
 
-def workspace_layout(num_tokens: int) -> MiMoeLayout:
+def workspace_layout(num_tokens: int, shape=DEFAULT_SHAPE) -> MiMoeLayout:
     out = MiMoeLayout()
-    check(lib().mi_moe_workspace_layout(int(num_tokens), ctypes.byref(out)))
+    L = lib(shape)
+    check(L.mi_moe_workspace_layout(int(num_tokens), ctypes.byref(out)), L)
     return out

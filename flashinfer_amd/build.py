@@ -1,5 +1,7 @@
-"""Builds libmi_moe.so (all HIP kernels + the C ABI) and libmi_peaks.so
-(achievable-peak probes used by bench.py) for gfx950 with hipcc.
+"""Builds libmi_moe.so (all HIP kernels + the C ABI, for the default
+H=7168, I=2048), one libmi_moe_h<H>_i<I>.so per further shape in
+shapes.SHAPES, and libmi_peaks.so (achievable-peak probes used by bench.py),
+for gfx950 with hipcc.
 
 Usage: python -m flashinfer_amd.build [--jobs N] [--save-temps]
 The shared libraries land next to this file so they travel with the tree.
@@ -12,6 +14,8 @@ import shutil
 import subprocess
 import sys
 from concurrent.futures import ThreadPoolExecutor
+
+from .shapes import SHAPES, lib_name
 
 HERE = os.path.dirname(os.path.abspath(__file__))
 CSRC = os.path.join(HERE, "csrc")
@@ -51,9 +55,12 @@ def hipcc() -> str:
     return path
 
 
-def _compile(src: str, extra) -> str:
-    obj = os.path.join(BUILD, src.replace(".hip", ".o"))
-    cmd = [hipcc(), *HIPCC_FLAGS, *SOURCE_FLAGS.get(src, []), *extra,
+def _compile(src: str, extra, shape=None) -> str:
+    sub = os.path.join(BUILD, f"h{shape[0]}_i{shape[1]}" if shape else "common")
+    os.makedirs(sub, exist_ok=True)
+    obj = os.path.join(sub, src.replace(".hip", ".o"))
+    defs = [f"-DMI_MOE_HIDDEN={shape[0]}", f"-DMI_MOE_INTER={shape[1]}"] if shape else []
+    cmd = [hipcc(), *HIPCC_FLAGS, *SOURCE_FLAGS.get(src, []), *defs, *extra,
            "-I", os.path.join(HERE, "..", "include"),
            "-c", os.path.join(CSRC, src), "-o", obj]
     r = subprocess.run(cmd, capture_output=True, text=True)
@@ -67,8 +74,10 @@ def _compile(src: str, extra) -> str:
 
 def _link(objs, out):
     tmp = out + ".tmp"
+    # -Bsymbolic: each shape's library binds its own kernels and helpers even
+    # when several (same C++ names, other shape constants) share a process
     cmd = [hipcc(), f"--offload-arch={ARCH}", "-mcode-object-version=5", "-shared", "-fPIC",
-           *objs, "-o", tmp]
+           "-Wl,-Bsymbolic", *objs, "-o", tmp]
     r = subprocess.run(cmd, capture_output=True, text=True)
     if r.returncode != 0:
         raise RuntimeError(f"link of {os.path.basename(out)} failed:\n{r.stderr}")
@@ -77,10 +86,13 @@ def _link(objs, out):
 
 def build(jobs: int = 8, extra=()) -> str:
     os.makedirs(BUILD, exist_ok=True)
+    jobs_list = [(s, shape) for shape in SHAPES for s in SOURCES] + [(s, None) for s in PEAKS_SOURCES]
     with ThreadPoolExecutor(max_workers=jobs) as ex:
-        objs = list(ex.map(lambda s: _compile(s, list(extra)), SOURCES + PEAKS_SOURCES))
-    _link(objs[:len(SOURCES)], LIB)
-    _link(objs[len(SOURCES):], PEAKS_LIB)
+        objs = list(ex.map(lambda j: _compile(j[0], list(extra), j[1]), jobs_list))
+    n = len(SOURCES)
+    for k, shape in enumerate(SHAPES):
+        _link(objs[k * n:(k + 1) * n], os.path.join(HERE, lib_name(*shape)))
+    _link(objs[len(SHAPES) * n:], PEAKS_LIB)
     return LIB
 
 

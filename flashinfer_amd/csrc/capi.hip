@@ -136,7 +136,11 @@ int mi_moe_workspace_layout(int64_t num_tokens, mi_moe_layout* out) {
 
 const char* mi_moe_last_error(void) { return g_last_error.c_str(); }
 
-const char* mi_moe_version(void) { return "mi_moe 0.1.0 gfx950"; }
+#define MI_MOE_STR2(x) #x
+#define MI_MOE_STR(x) MI_MOE_STR2(x)
+const char* mi_moe_version(void) {
+    return "mi_moe 0.1.0 gfx950 h" MI_MOE_STR(MI_MOE_HIDDEN) " i" MI_MOE_STR(MI_MOE_INTER);
+}
 
 int mi_moe_route(const float* routing_logits, const void* routing_bias, int32_t bias_dtype,
                  int64_t num_tokens, float routed_scaling_factor, int32_t* topk_ids,
@@ -160,6 +164,15 @@ int mi_moe_route(const float* routing_logits, const void* routing_bias, int32_t 
                                   (hipStream_t)stream);
     if (err != hipSuccess)
         return fail(MI_MOE_ERR_HIP, "mi_moe_route: launch failed: %s", hipGetErrorString(err));
+    return MI_MOE_OK;
+}
+
+int mi_moe_shape(int32_t* hidden_size, int32_t* intermediate_size) {
+    g_last_error.clear();
+    if (!hidden_size || !intermediate_size)
+        return fail(MI_MOE_ERR_INVALID, "mi_moe_shape: NULL pointer argument");
+    *hidden_size = H;
+    *intermediate_size = I;
     return MI_MOE_OK;
 }
 

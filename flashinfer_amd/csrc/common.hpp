@@ -7,9 +7,21 @@
 
 namespace mimoe {
 
-// Problem shape of the definition (solution/triton/kernel.py:615-625).
-constexpr int H = 7168;        // hidden size
-constexpr int I = 2048;        // intermediate size
+// Problem shape (solution/triton/kernel.py:615-625 hard-codes H=7168,
+// I=2048). H and I are compile-time constants of each library build
+// (-DMI_MOE_HIDDEN / -DMI_MOE_INTER); routing, the 32 local experts and the
+// 128-element scale blocks are fixed by the ds-routing definition family.
+#ifndef MI_MOE_HIDDEN
+#define MI_MOE_HIDDEN 7168
+#endif
+#ifndef MI_MOE_INTER
+#define MI_MOE_INTER 2048
+#endif
+constexpr int H = MI_MOE_HIDDEN;  // hidden size
+constexpr int I = MI_MOE_INTER;   // intermediate size
+// combine: 1024-column chunks; GEMM1 K split over 4 waves of 2-deep rings:
+// 8 | H/128. GEMM2 rings at least 2 deep, tiles of 128 columns: 2 | I/128.
+static_assert(H % 1024 == 0 && I % 256 == 0, "supported shapes: H % 1024 == 0, I % 256 == 0");
 constexpr int N1 = 2 * I;      // GEMM1 output width (gate | up)
 constexpr int EG = 256;        // global experts
 constexpr int EL = 32;         // local experts per shard
@@ -18,9 +30,9 @@ constexpr int NGROUP = 8;
 constexpr int KGROUP = 4;
 constexpr int GSIZE = EG / NGROUP;  // 32
 constexpr int BLK = 128;            // scale block
-constexpr int HB = H / BLK;         // 56 k-blocks of GEMM1
-constexpr int IB = I / BLK;         // 16 k-blocks of GEMM2
-constexpr int N1B = N1 / BLK;       // 32 n-blocks of GEMM1
+constexpr int HB = H / BLK;         // k-blocks of GEMM1 (56 at H=7168)
+constexpr int IB = I / BLK;         // k-blocks of GEMM2 (16 at I=2048)
+constexpr int N1B = N1 / BLK;       // n-blocks of GEMM1 (32 at I=2048)
 
 // Device pointers into the caller's workspace plus the call's scalars.
 struct Plan {
@@ -34,8 +46,8 @@ struct Plan {
     float* sorted_w;           // [8T]
     int* tok_slot;             // [T, 8]
     int* chunk_cnt;            // [ceil(T/1024), 32] per-chunk expert totals (large-T sort)
-    uint16_t* act;             // bf16 [8T, 2048]
-    uint16_t* part;            // bf16 [8T, 7168]: routing weight x GEMM2 row of each slot
+    uint16_t* act;             // bf16 [8T, I]
+    uint16_t* part;            // bf16 [8T, H]: routing weight x GEMM2 row of each slot
 };
 
 constexpr int META_EXPERT_OFF = 0;

@@ -165,8 +165,10 @@ int gemm2_bm(int variant) {
 
 template <int MT, int D, int NW, int NQ>
 static void launch_stream2(const Plan& p, const uint8_t* w2, const float* w2s, hipStream_t s) {
+    // a ring deeper than the shape's k-blocks allow falls back to 2 deep
+    constexpr int DD = IB % D == 0 ? D : 2;
     dim3 grid(H / (16 * NQ * NW), max_mtiles(p.T, 16 * MT));
-    hipLaunchKernelGGL((gemm2_stream_kernel<MT, D, NW, NQ>), grid, dim3(64 * NW), 0, s, p, w2, w2s);
+    hipLaunchKernelGGL((gemm2_stream_kernel<MT, DD, NW, NQ>), grid, dim3(64 * NW), 0, s, p, w2, w2s);
 }
 
 hipError_t launch_gemm2(const Plan& p, const uint8_t* w2, const float* w2s, int variant,

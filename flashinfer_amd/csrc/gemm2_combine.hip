@@ -8,7 +8,7 @@
 //
 // A workgroup owns 16 output columns for every local expert: its 4 waves take
 // the 16-slot row tiles round-robin (tile u goes to wave u % 4) and stream the
-// matching 16 x 2048 fp8 weight rows through a D-deep register ring that runs
+// matching 16 x I fp8 weight rows through a D-deep register ring that runs
 // across tile boundaries. At the end of a tile each lane adds w_s * result
 // into a per-wave fp32 accumulator [T][16] in LDS (a tile never holds the
 // same token twice, and one wave handles its tiles in order, so the
@@ -41,6 +41,7 @@ __global__ __launch_bounds__(256) void gemm2_combine_kernel(Plan p, const uint8_
                                                             const float* __restrict__ w2s,
                                                             uint16_t* __restrict__ out) {
     static_assert(IB % D == 0, "ring depth must divide the k-blocks of a tile");
+    static_assert(D < IB && IB <= 64, "the load side stays in the tile; one lane per k-block scale");
     extern __shared__ float acc_lds[];  // [4 waves][T][16]
     const int T = p.T;
     const int tid = threadIdx.x;
@@ -64,7 +65,7 @@ __global__ __launch_bounds__(256) void gemm2_combine_kernel(Plan p, const uint8_
         // Per-tile data, fetched when the load side enters a tile (D steps
         // before the compute side needs it): block scales of the 16 k-blocks,
         // and the token and routing weight of the lane's 4 output rows.
-        // Lane q < 16 holds the scale of k-block q; readlane picks it.
+        // Lane q < IB holds the scale of k-block q; readlane picks it.
         UnitInfo lu = unit_info(p.meta, wave);
         float lu_sb = 0.f;
         int lu_tok[4];
@@ -77,7 +78,7 @@ __global__ __launch_bounds__(256) void gemm2_combine_kernel(Plan p, const uint8_
 
         auto fetch_unit = [&](int u) __attribute__((always_inline)) {
             lu = unit_info(p.meta, u);
-            lu_sb = w2s[((size_t)lu.e * HB + nb) * IB + (lane & (IB - 1))];
+            lu_sb = w2s[((size_t)lu.e * HB + nb) * IB + lane % IB];
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
                 const int row = g * 4 + i;
@@ -87,8 +88,8 @@ __global__ __launch_bounds__(256) void gemm2_combine_kernel(Plan p, const uint8_
             }
         };
         auto load = [&](int d, int s) __attribute__((always_inline)) {
-            const int kb = s & (IB - 1);
-            if (kb == 0 && s > 0) fetch_unit(wave + 4 * (s >> 4));
+            const int kb = s % IB;  // step s: k-block kb of the wave's tile s / IB
+            if (kb == 0 && s > 0) fetch_unit(wave + 4 * (s / IB));
             const uint8_t* bp = w2 + ((size_t)lu.e * H + n0 + r) * I + g * 16 + kb * BLK;
             b[d] = ld_frag(bp);
             const uint16_t* ap =
@@ -99,7 +100,7 @@ __global__ __launch_bounds__(256) void gemm2_combine_kernel(Plan p, const uint8_
             a[d][3] = ld16(ap + 72);
         };
         auto compute = [&](int d, int s) __attribute__((always_inline)) {
-            const int kb = s & (IB - 1);
+            const int kb = s % IB;
             if (kb == 0) {
                 // The load side is D < IB steps ahead, so it is still in this tile.
                 cu = lu;
@@ -163,7 +164,8 @@ hipError_t launch_gemm2_combine(const Plan& p, const uint8_t* w2, const float* w
                                 hipStream_t s) {
     if (p.T <= 0) return hipSuccess;
     const size_t lds = (size_t)4 * p.T * 16 * sizeof(float);
-    hipLaunchKernelGGL((gemm2_combine_kernel<4>), dim3(H / 16), dim3(256), lds, s, p, w2, w2s, out);
+    constexpr int D = IB % 4 == 0 ? 4 : 2;  // ring depth must divide the shape's k-blocks
+    hipLaunchKernelGGL((gemm2_combine_kernel<D>), dim3(H / 16), dim3(256), lds, s, p, w2, w2s, out);
     return hipGetLastError();
 }
 

@@ -23,6 +23,8 @@ import torch
 
 from . import _lib
 
+# Default shape (kernel.py:615-625); run() takes H and I from the weights and
+# uses the library built for them (flashinfer_amd/shapes.py).
 H, I, E_GLOBAL, E_LOCAL, BLOCK = 7168, 2048, 256, 32, 128
 FP8 = torch.float8_e4m3fn
 
@@ -39,6 +41,16 @@ def _workspace(device: torch.device, stream: int, nbytes: int) -> torch.Tensor:
         ws = torch.empty(size, dtype=torch.uint8, device=device)
         _workspaces[key] = ws
     return ws
+
+
+def _shape_of(gemm1_weights) -> tuple:
+    """(H, I) from gemm1_weights [32, 2I, H]: the shape whose library runs the call."""
+    if not isinstance(gemm1_weights, torch.Tensor) or gemm1_weights.dim() != 3:
+        raise ValueError("gemm1_weights must be a 3-D tensor [32, 2I, H]")
+    two_i, h = int(gemm1_weights.shape[1]), int(gemm1_weights.shape[2])
+    if two_i % 2:
+        raise ValueError(f"gemm1_weights: dimension 1 ({two_i}) must be 2I (even)")
+    return (h, two_i // 2)
 
 
 def _expect(t: torch.Tensor, name: str, dtypes, shape) -> None:
@@ -82,6 +94,7 @@ def _phase_timing_enabled() -> bool:
 
 
 def _emit_phase_timing(args, T: int) -> None:
+    shape = _shape_of(args[4])
     global _PHASE_TIMING_EMITTED
     device = args[-1].device
     with torch.cuda.device(device):
@@ -92,7 +105,7 @@ def _emit_phase_timing(args, T: int) -> None:
                   for i, name in enumerate(_lib.PHASES)}
         slots = 0
         if T > 0:
-            L = _lib.workspace_layout(T)
+            L = _lib.workspace_layout(T, shape)
             meta = last_workspace(device)[L.expert_off:L.expert_off + (E_LOCAL + 1) * 4]
             slots = int(meta.view(torch.int32)[E_LOCAL].item())
     phase_ms = {ref: sum(native[n] for n in names) for ref, names in _REFERENCE_PHASES}
@@ -151,6 +164,8 @@ def _call(routing_logits, routing_bias, hidden_states, hidden_states_scale, gemm
     if not isinstance(routing_logits, torch.Tensor) or routing_logits.dim() != 2:
         raise ValueError("routing_logits must be a 2-D tensor [T, 256]")
     T = int(routing_logits.shape[0])
+    shape = _shape_of(gemm1_weights)
+    H, I = shape
     _expect(routing_logits, "routing_logits", (torch.float32,), (T, E_GLOBAL))
     _expect(routing_bias, "routing_bias", (torch.bfloat16, torch.float32), (E_GLOBAL,))
     _expect(hidden_states, "hidden_states", (FP8,), (T, H))
@@ -182,7 +197,8 @@ def _call(routing_logits, routing_bias, hidden_states, hidden_states_scale, gemm
     with torch.cuda.device(device):
         cur = torch.cuda.current_stream(device)
         stream = cur.cuda_stream
-        need = _lib.workspace_size(T)
+        L = _lib.lib(shape)
+        need = _lib.workspace_size(T, shape)
         ws = _workspace(device, stream, need)
         args = _lib.MiMoeArgs(
             routing_logits=ins[0].data_ptr(), routing_bias=ins[1].data_ptr(),
@@ -195,7 +211,7 @@ def _call(routing_logits, routing_bias, hidden_states, hidden_states_scale, gemm
                         else _lib.MI_MOE_DTYPE_F32),
             reserved=0, workspace=ws.data_ptr(), workspace_bytes=ws.numel())
         if events is None:
-            _lib.check(_lib.lib().mi_moe_run(ctypes.byref(args), ctypes.c_void_p(stream)))
+            _lib.check(L.mi_moe_run(ctypes.byref(args), ctypes.c_void_p(stream)), L)
         else:
             handles = []
             for ev in events:
@@ -203,8 +219,8 @@ def _call(routing_logits, routing_bias, hidden_states, hidden_states_scale, gemm
                     ev.record(cur)
                 handles.append(ev.cuda_event)
             arr = (ctypes.c_void_p * len(handles))(*handles)
-            _lib.check(_lib.lib().mi_moe_run_profiled(ctypes.byref(args), ctypes.c_void_p(stream),
-                                                      arr, len(handles)))
+            _lib.check(L.mi_moe_run_profiled(ctypes.byref(args), ctypes.c_void_p(stream),
+                                             arr, len(handles)), L)
     if out is not output:
         output.copy_(out)
 
@@ -269,13 +285,19 @@ def sort(topk_ids: torch.Tensor, topk_weights: torch.Tensor, local_expert_offset
 
 def quantize_activations(hidden: torch.Tensor, hidden_states: torch.Tensor | None = None,
                          hidden_states_scale: torch.Tensor | None = None):
-    """FP8 activation quantiser feeding ``run``: bf16 ``hidden`` [T, 7168] ->
-    (``hidden_states`` fp8 e4m3fn [T, 7168], ``hidden_states_scale`` fp32
-    [56, T]), the input pair of kernel.py:600-613 in its block-major scale
-    layout (kernel.py:169). Per token and 128-element block:
-    s = max(amax, 1e-10) / 448, q = e4m3(clamp(x / s, -448, 448)), round to
-    nearest even. Inputs must be finite. Outputs may be passed in."""
-    T = int(hidden.shape[0]) if isinstance(hidden, torch.Tensor) and hidden.dim() == 2 else -1
+    """FP8 activation quantiser feeding ``run``: bf16 ``hidden`` [T, H] ->
+    (``hidden_states`` fp8 e4m3fn [T, H], ``hidden_states_scale`` fp32
+    [H/128, T]), the input pair of kernel.py:600-613 in its block-major scale
+    layout (kernel.py:169); H = 7168 or another built hidden size. Per token
+    and 128-element block: s = max(amax, 1e-10) / 448,
+    q = e4m3(clamp(x / s, -448, 448)), round to nearest even. Inputs must be
+    finite. Outputs may be passed in."""
+    if not isinstance(hidden, torch.Tensor) or hidden.dim() != 2:
+        raise ValueError("hidden must be a 2-D tensor [T, H]")
+    T, H = int(hidden.shape[0]), int(hidden.shape[1])
+    shape = next((sh for sh in _lib.built_shapes() if sh[0] == H), None)
+    if shape is None:
+        raise ValueError(f"no library for hidden size {H} (built: {_lib.built_shapes()})")
     _expect(hidden, "hidden", (torch.bfloat16,), (T, H))
     dev = hidden.device
     if hidden_states is None:
@@ -296,9 +318,10 @@ def quantize_activations(hidden: torch.Tensor, hidden_states: torch.Tensor | Non
     x = hidden.contiguous()
     with torch.cuda.device(dev):
         stream = torch.cuda.current_stream(dev).cuda_stream
-        _lib.check(_lib.lib().mi_moe_quantize_fp8(
+        L = _lib.lib(shape)
+        _lib.check(L.mi_moe_quantize_fp8(
             x.data_ptr(), T, hidden_states.data_ptr(), hidden_states_scale.data_ptr(),
-            ctypes.c_void_p(stream)))
+            ctypes.c_void_p(stream)), L)
     return hidden_states, hidden_states_scale
 
 

@@ -5,7 +5,10 @@
  * expert-parallel shard of 32 local experts, definition
  * moe_fp8_block_scale_ds_routing_topk8_ng8_kg4_e32_h7168_i2048
  * (H = 7168, I = 2048, 256 global experts in 8 groups of 32, top-4 groups,
- * top-8 experts, 128-element scale blocks).
+ * top-8 experts, 128-element scale blocks). The shapes below are written for
+ * that H and I; a library built for another (H, I) (mi_moe_shape) takes the
+ * same layouts with 7168 -> H, 2048 -> I, 4096 -> 2I, 56 -> H/128,
+ * 32 (GEMM1 n-blocks) -> 2I/128 and 16 -> I/128.
  *
  * All pointers are device pointers; the caller owns every buffer, including
  * the workspace. The library never allocates device memory, never
@@ -122,6 +125,12 @@ int mi_moe_sort(const int32_t* topk_ids, const float* topk_weights, int64_t num_
  * kernel.py:600-613. Pointers 16-byte aligned (scale: 4-byte). */
 int mi_moe_quantize_fp8(const void* hidden_bf16, int64_t num_tokens, uint8_t* hidden_states,
                         float* hidden_states_scale, void* stream);
+
+/* Hidden size H and expert intermediate size I this library is compiled for
+ * (kernel.py:615-625 hard-codes 7168 and 2048; libmi_moe.so is that shape,
+ * libmi_moe_h<H>_i<I>.so others). Every tensor shape of mi_moe_args follows
+ * from them; no counterpart in the reference. */
+int mi_moe_shape(int32_t* hidden_size, int32_t* intermediate_size);
 
 /* Message of the last error on the calling thread ("" if none). */
 const char* mi_moe_last_error(void);

@@ -17,18 +17,24 @@ def log(msg: str) -> None:
     print(f"[{time.strftime('%H:%M:%S')}] {msg}", file=sys.stderr, flush=True)
 
 
-def device_weights(device="cuda"):
-    if device not in _DEV_WEIGHTS:
+def device_weights(device="cuda", H=W.H_DEF, I=W.I_DEF):
+    """Device copies of the seeded weights of shape (H, I), one per device and
+    shape; a second shape evicts the first (only one fits comfortably)."""
+    key = (device, H, I)
+    if key not in _DEV_WEIGHTS:
+        for k in [k for k in _DEV_WEIGHTS if k[0] == device]:
+            del _DEV_WEIGHTS[k]
         t0 = time.time()
-        w = W.make_weights()
-        _DEV_WEIGHTS[device] = {k: v.to(device) for k, v in w.items()}
-        log(f"weights generated and copied in {time.time() - t0:.1f}s")
-    return _DEV_WEIGHTS[device]
+        w = W.make_weights(H, I)
+        _DEV_WEIGHTS[key] = {k: v.to(device) for k, v in w.items()}
+        log(f"weights (H={H}, I={I}) generated and copied in {time.time() - t0:.1f}s")
+    return _DEV_WEIGHTS[key]
 
 
 def gpu_args(wl: W.Workload, device="cuda"):
-    dw = device_weights(device)
     t = wl.tensors
+    w1 = t["gemm1_weights"]
+    dw = device_weights(device, int(w1.shape[2]), int(w1.shape[1]) // 2)
     return [t["routing_logits"].to(device), t["routing_bias"].to(device),
             t["hidden_states"].to(device), t["hidden_states_scale"].to(device),
             dw["gemm1_weights"], dw["gemm1_weights_scale"], dw["gemm2_weights"],
@@ -38,7 +44,7 @@ def gpu_args(wl: W.Workload, device="cuda"):
 def run_gpu(wl: W.Workload, device="cuda", fill=None):
     from flashinfer_amd import kernel
     args = gpu_args(wl, device)
-    out = torch.empty(wl.T, W.H_DEF, dtype=torch.bfloat16, device=device)
+    out = torch.empty(wl.T, wl.tensors["gemm1_weights"].shape[2], dtype=torch.bfloat16, device=device)
     if fill is not None:
         out.fill_(fill)
     kernel.run(*args, out)

@@ -173,3 +173,28 @@ def test_phase_timing_switch(monkeypatch):
     monkeypatch.setenv("FIB_PROFILE_PHASES", "1")
     monkeypatch.setattr(kernel, "_PHASE_TIMING_EMITTED", True)
     assert not kernel._phase_timing_enabled()
+
+
+@pytest.mark.parametrize("shape", [(7168, 2048), (4096, 1536)])
+def test_each_shape_library_reports_shape_and_exports(shape):
+    """Every built (H, I) library loads next to the default one, says which
+    shape it is, exports the whole declared ABI and sizes its workspace by it."""
+    from flashinfer_amd import shapes
+    assert shape in shapes.SHAPES and shapes.supported(*shape)
+    L = _lib.lib(shape)
+    h, i = ctypes.c_int32(), ctypes.c_int32()
+    assert L.mi_moe_shape(ctypes.byref(h), ctypes.byref(i)) == _lib.MI_MOE_OK
+    assert (h.value, i.value) == shape
+    assert f"h{shape[0]} i{shape[1]}" in L.mi_moe_version().decode()
+    for name in _declared_functions():
+        assert hasattr(L, name), name
+    lay = _lib.workspace_layout(100, shape)
+    assert lay.part - lay.act >= 800 * shape[1] * 2  # act rows of I bf16 for 8T slots
+    assert lay.total - lay.part >= 800 * shape[0] * 2
+
+
+def test_unbuilt_shape_is_refused():
+    with pytest.raises(ValueError, match="no library"):
+        _lib.lib((2048, 768))
+    with pytest.raises(ValueError, match="H % 1024"):
+        _lib.lib((7000, 2048))
