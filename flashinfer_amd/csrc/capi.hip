@@ -5,7 +5,8 @@
 // nothing and reports why through mi_moe_last_error(). The call enqueues
 // route -> sort -> GEMM1+SwiGLU -> GEMM2 -> combine on the caller's stream
 // with grids sized from T alone: no device-to-host copy, no host sync
-// (the reference syncs three times, kernel.py:572, :718, :773).
+// (the reference syncs three times, kernel.py:572, :718, :773). Small T folds
+// route and sort into one launch (T <= 8) or the sort into GEMM1 (T <= 64).
 #include <math.h>
 #include <stdarg.h>
 #include <stdio.h>
@@ -93,6 +94,16 @@ bool fuse_front_end(int64_t T) {
     const char* env = getenv("MI_MOE_FUSE_FRONT");
     if (env && *env) f = atoi(env) != 0;
     return f && route_sort_supported((int)T);
+}
+
+// GEMM1 does the sort's work itself (no sort launch) where it can: the
+// K-split stream variant at T <= 64 without the fused front end
+// (MI_MOE_SORT_IN_GEMM1=0/1 overrides).
+bool sort_in_gemm1(int64_t T, int g1) {
+    bool f = true;
+    const char* env = getenv("MI_MOE_SORT_IN_GEMM1");
+    if (env && *env) f = atoi(env) != 0;
+    return f && !fuse_front_end(T) && gemm1_sorts_supported((int)T, g1);
 }
 
 Variants pick_variants(int64_t T) {
@@ -271,6 +282,7 @@ static int run_impl(const mi_moe_args* a, hipStream_t s, hipEvent_t const* ev) {
         if (ev && err == hipSuccess) err = hipEventRecord(ev[i], s);
     };
     const int bias_f32 = a->bias_dtype == MI_MOE_DTYPE_F32;
+    const bool g1_sorts = sort_in_gemm1(T, var.g1);
     mark(0);
     if (fuse_front_end(T)) {
         if (err == hipSuccess)
@@ -282,12 +294,19 @@ static int run_impl(const mi_moe_args* a, hipStream_t s, hipEvent_t const* ev) {
             err = launch_route(a->routing_logits, a->routing_bias, bias_f32, p.T, p.rsf,
                                p.topk_ids, p.topk_w, s);
         mark(1);
-        if (err == hipSuccess) err = launch_sort(p, gemm1_bm(var.g1), gemm2_bm(var.g2), s);
+        if (err == hipSuccess && !g1_sorts)
+            err = launch_sort(p, gemm1_bm(var.g1), gemm2_bm(var.g2), s);
     }
     mark(2);
-    if (err == hipSuccess)
-        err = launch_gemm1(p, a->hidden_states, a->hidden_states_scale, a->gemm1_weights,
-                           a->gemm1_weights_scale, var.g1, s);
+    if (err == hipSuccess) {
+        if (g1_sorts)
+            err = launch_gemm1_sorting(p, a->hidden_states, a->hidden_states_scale,
+                                       a->gemm1_weights, a->gemm1_weights_scale, gemm1_bm(var.g1),
+                                       gemm2_bm(var.g2), s);
+        else
+            err = launch_gemm1(p, a->hidden_states, a->hidden_states_scale, a->gemm1_weights,
+                               a->gemm1_weights_scale, var.g1, s);
+    }
     mark(3);
     const bool fused = var.g2 == VARIANT_GEMM2_COMBINE && gemm2_combine_supported(p.T);
     if (err == hipSuccess) {

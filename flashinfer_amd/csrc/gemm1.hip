@@ -22,38 +22,63 @@
 // [16g, 16g+16) and [64+16g, 64+16g+16) of the 128-byte k-block, g = l / 16.
 // A and B use the same mapping, so the k pairing inside the MFMA is exact
 // whatever order the instruction assigns to the 32 bytes of a lane.
-#include "common.hpp"
+//
+// With SORT (T <= 64, MT = 1) the kernel also stands in for the sort launch:
+// each wave derives its row tile and its rows' tokens from the top-k ids
+// (wave_tile: the one-wave sort's counts and scan, in registers), so no
+// kernel boundary separates routing from GEMM1, and workgroup (0, 0) writes
+// the sort's tables (expert offsets, tile prefixes for bm1 / bm2, slot lists)
+// for GEMM2 and the combine, which run after this kernel.
+#include "sort_impl.hpp"
 
 namespace mimoe {
 
-template <int MT, int D, int NW, int KS = 1>
-__global__ __launch_bounds__(64 * NW * KS) void gemm1_stream_kernel(Plan p, const uint8_t* __restrict__ hs,
+template <int MT, int D, int NW, int KS = 1, bool SORT = false>
+__global__ __launch_bounds__(64 * NW * KS) __attribute__((amdgpu_waves_per_eu(SORT ? 5 : 1)))
+void gemm1_stream_kernel(Plan p, const uint8_t* __restrict__ hs,
                                                                     const float* __restrict__ hs_scale,
                                                                     const uint8_t* __restrict__ w1,
-                                                                    const float* __restrict__ w1s) {
+                                                                    const float* __restrict__ w1s,
+                                                                    int bm1, int bm2) {
     constexpr int KB = HB / KS;  // k-blocks per wave
     static_assert(HB % KS == 0 && KB % D == 0, "k split and prefetch depth must divide the k-blocks");
+    static_assert(!SORT || MT == 1, "the in-kernel sort gives each lane the token of one row");
     constexpr int BM = 16 * MT;
     __shared__ float sa_lds[HB][BM];
     // partial sums of waves 1..KS-1 of a column group: [split-1][group][value][lane]
     __shared__ float red[KS > 1 ? KS - 1 : 1][NW][KS > 1 ? 8 * MT : 1][64];
 
-    int e, row0, nrows;
-    if (!find_tile(p.meta, META_MTILE1, blockIdx.y, BM, e, row0, nrows)) return;
-
     const int tid = threadIdx.x;
     const int lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int r = lane & 15, g = lane >> 4;
+
+    // Row tile and the tokens of this lane's rows (row i * 16 + r).
+    int e, row0, nrows;
+    int tok[MT];
+    if constexpr (SORT) {
+        const WaveTile wt = wave_tile(p, lane, blockIdx.y, BM);
+        if (blockIdx.x == 0 && blockIdx.y == 0 && wave == 0)
+            sort_one_wave<1>(p, p.topk_ids, p.topk_w, bm1, bm2, lane);
+        if (!wt.valid) return;  // the same for every wave of the workgroup
+        e = wt.e;
+        row0 = wt.row0;
+        nrows = wt.nrows;
+        tok[0] = nth_set_bit(wt.hits, wt.rank0 + min(r, nrows - 1));
+    } else {
+        if (!find_tile(p.meta, META_MTILE1, blockIdx.y, BM, e, row0, nrows)) return;
+#pragma unroll
+        for (int i = 0; i < MT; ++i) tok[i] = p.sorted_tok[row0 + min(i * 16 + r, nrows - 1)];
+    }
+
     const int wc = wave % NW;         // column group
     const int ks = wave / NW;         // k split: k-blocks [ks*KB, ks*KB + KB)
     const int j0 = blockIdx.x * (16 * NW) + wc * 16;
-    const int r = lane & 15, g = lane >> 4;
     const uint8_t* bg_ptr = w1 + ((size_t)e * N1 + j0 + r) * H + (size_t)ks * KB * BLK + g * 16;
     const uint8_t* bu_ptr = w1 + ((size_t)e * N1 + I + j0 + r) * H + (size_t)ks * KB * BLK + g * 16;
     const uint8_t* a_ptr[MT];
 #pragma unroll
-    for (int i = 0; i < MT; ++i)
-        a_ptr[i] = hs + (size_t)p.sorted_tok[row0 + min(i * 16 + r, nrows - 1)] * H + ks * KB * BLK + g * 16;
+    for (int i = 0; i < MT; ++i) a_ptr[i] = hs + (size_t)tok[i] * H + ks * KB * BLK + g * 16;
     const float* sbg_ptr = w1s + ((size_t)e * N1B + j0 / BLK) * HB + ks * KB;
     const float* sbu_ptr = w1s + ((size_t)e * N1B + (I + j0) / BLK) * HB + ks * KB;
     const float (*sa_k)[BM] = sa_lds + ks * KB;  // this wave's k-blocks
@@ -96,9 +121,15 @@ __global__ __launch_bounds__(64 * NW * KS) void gemm1_stream_kernel(Plan p, cons
     // LDS while those loads are in flight.
 #pragma unroll
     for (int d = 0; d < D; ++d) load(d, d);
-    for (int i = tid; i < HB * BM; i += 64 * NW * KS) {
-        const int kb = i / BM, m = i % BM;
-        sa_lds[kb][m] = hs_scale[(size_t)kb * p.T + p.sorted_tok[row0 + min(m, nrows - 1)]];
+    // (64 * NW * KS is a multiple of BM, so entry i's row m = i % BM is the
+    // same for all of a thread's entries: row tid % BM = i' * 16 + r.)
+    static_assert((64 * NW * KS) % BM == 0, "scale loader row");
+    {
+        const int tok_m = tok[(tid % BM) / 16];
+        for (int i = tid; i < HB * BM; i += 64 * NW * KS) {
+            const int kb = i / BM, m = i % BM;
+            sa_lds[kb][m] = hs_scale[(size_t)kb * p.T + tok_m];
+        }
     }
     __syncthreads();
 
@@ -167,12 +198,23 @@ int gemm1_bm(int variant) {
     }
 }
 
-template <int MT, int D, int NW, int KS = 1>
+template <int MT, int D, int NW, int KS = 1, bool SORT = false>
 static void launch_stream1(const Plan& p, const uint8_t* hs, const float* hs_scale,
-                           const uint8_t* w1, const float* w1s, hipStream_t s) {
+                           const uint8_t* w1, const float* w1s, hipStream_t s, int bm1 = 0,
+                           int bm2 = 0) {
     dim3 grid(I / (16 * NW), max_mtiles(p.T, 16 * MT));
-    hipLaunchKernelGGL((gemm1_stream_kernel<MT, D, NW, KS>), grid, dim3(64 * NW * KS), 0, s, p, hs,
-                       hs_scale, w1, w1s);
+    hipLaunchKernelGGL((gemm1_stream_kernel<MT, D, NW, KS, SORT>), grid, dim3(64 * NW * KS), 0, s, p,
+                       hs, hs_scale, w1, w1s, bm1, bm2);
+}
+
+bool gemm1_sorts_supported(int T, int variant) { return variant == 16 && T > 0 && T <= SMALL_T; }
+
+hipError_t launch_gemm1_sorting(const Plan& p, const uint8_t* hs, const float* hs_scale,
+                                const uint8_t* w1, const float* w1s, int bm1, int bm2,
+                                hipStream_t s) {
+    if (p.T <= 0) return hipSuccess;
+    launch_stream1<1, 2, 1, 4, true>(p, hs, hs_scale, w1, w1s, s, bm1, bm2);
+    return hipGetLastError();
 }
 
 hipError_t launch_gemm1(const Plan& p, const uint8_t* hs, const float* hs_scale, const uint8_t* w1,

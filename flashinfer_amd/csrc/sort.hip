@@ -19,79 +19,15 @@
 // T <= 1024 (sort_kernel); either with the routing done in place for small T
 // (route_sort_kernel, one launch for the whole front end); and for large T a
 // per-chunk count kernel plus a per-chunk place kernel that scans the chunk
-// totals itself.
+// totals itself. At decode sizes the K-split GEMM1 kernel can take the sort's
+// place instead: each of its waves finds its row tile from the top-k ids, and
+// one workgroup writes these tables for GEMM2 and the combine (gemm1.hip).
 #include "route_impl.hpp"
+#include "sort_impl.hpp"
 
 namespace mimoe {
 
 constexpr int CHUNK = 1024;
-
-// A token's local experts: bit mask over the 32 local ids, and per top-k
-// position the local id (-1 if not local) and routing weight.
-struct TokLocal {
-    uint32_t m;
-    int lid[TOPK];
-    float lw[TOPK];
-};
-
-__device__ __forceinline__ TokLocal make_local(const int ids[TOPK], const float ws[TOPK], int off) {
-    TokLocal r;
-    r.m = 0;
-#pragma unroll
-    for (int k = 0; k < TOPK; ++k) {
-        const int l = ids[k] - off;
-        const bool loc = (unsigned)l < (unsigned)EL;
-        r.lid[k] = loc ? l : -1;
-        r.lw[k] = ws[k];
-        r.m |= loc ? (1u << l) : 0u;
-    }
-    return r;
-}
-
-__device__ __forceinline__ TokLocal load_local(const int* ids_base, const float* w_base, int t,
-                                               bool valid, int off) {
-    int ids[TOPK];
-    float ws[TOPK];
-    if (valid) {
-        const int4 i0 = reinterpret_cast<const int4*>(ids_base + (size_t)t * TOPK)[0];
-        const int4 i1 = reinterpret_cast<const int4*>(ids_base + (size_t)t * TOPK)[1];
-        const float4 w0 = reinterpret_cast<const float4*>(w_base + (size_t)t * TOPK)[0];
-        const float4 w1 = reinterpret_cast<const float4*>(w_base + (size_t)t * TOPK)[1];
-        ids[0] = i0.x; ids[1] = i0.y; ids[2] = i0.z; ids[3] = i0.w;
-        ids[4] = i1.x; ids[5] = i1.y; ids[6] = i1.z; ids[7] = i1.w;
-        ws[0] = w0.x; ws[1] = w0.y; ws[2] = w0.z; ws[3] = w0.w;
-        ws[4] = w1.x; ws[5] = w1.y; ws[6] = w1.z; ws[7] = w1.w;
-    } else {
-#pragma unroll
-        for (int k = 0; k < TOPK; ++k) { ids[k] = -1 - EL; ws[k] = 0.f; }  // never local
-    }
-    return make_local(ids, ws, valid ? off : 0);
-}
-
-// Exclusive prefix of the per-expert slot counts held by lanes 0..31 of the
-// calling wave (every lane of the wave must call). Optionally writes the
-// expert offsets and the row-tile prefixes for GEMM tiles of bm1 / bm2 rows.
-__device__ __forceinline__ int scan_counts(const Plan& p, int lane, int c, int bm1, int bm2,
-                                           bool write) {
-    int v0 = c, v1 = (c + bm1 - 1) / bm1, v2 = (c + bm2 - 1) / bm2;
-    const int own0 = v0, own1 = v1, own2 = v2;
-#pragma unroll
-    for (int d = 1; d < EL; d <<= 1) {
-        const int u0 = __shfl_up(v0, d), u1 = __shfl_up(v1, d), u2 = __shfl_up(v2, d);
-        if (lane >= d) { v0 += u0; v1 += u1; v2 += u2; }
-    }
-    if (write && lane < EL) {
-        p.meta[META_EXPERT_OFF + lane] = v0 - own0;
-        p.meta[META_MTILE1 + lane] = v1 - own1;
-        p.meta[META_MTILE2 + lane] = v2 - own2;
-        if (lane == EL - 1) {
-            p.meta[META_EXPERT_OFF + EL] = v0;
-            p.meta[META_MTILE1 + EL] = v1;
-            p.meta[META_MTILE2 + EL] = v2;
-        }
-    }
-    return v0 - own0;
-}
 
 // Per-wave hit counts of the chunk into wcnt[wave][e] (lane e writes).
 __device__ __forceinline__ void wave_counts(const TokLocal& tl, int lane, int wave,
@@ -175,45 +111,7 @@ __device__ void sort_one_workgroup(const Plan& p, const int* ids_base, const flo
     place_with_prefix(p, tid, valid, tl, wcnt, lane, wave);
 }
 
-// T <= 64: one wave holds every token (lane t = token t). The expert counts
-// are popcounts of 32 ballots, the offsets a shuffle scan and the placement a
-// second round of ballots: no LDS and no barrier. Same slot order as
-// sort_one_workgroup (token-ascending inside an expert).
-constexpr int SMALL_T = 64;
-
-__device__ void sort_one_wave(const Plan& p, const int* ids_base, const float* w_base, int bm1,
-                              int bm2, int lane) {
-    const bool valid = lane < p.T;
-    const TokLocal tl = load_local(ids_base, w_base, lane, valid, p.local_offset);
-    int cnt = 0;
-#pragma unroll
-    for (int e = 0; e < EL; ++e) {
-        const unsigned long long bal = __ballot((tl.m >> e) & 1u);
-        if (lane == e) cnt = __popcll(bal);
-    }
-    const int off = scan_counts(p, lane, cnt, bm1, bm2, true);
-    const unsigned long long lower = (1ull << lane) - 1ull;
-    int j = 0;
-#pragma unroll
-    for (int e = 0; e < EL; ++e) {
-        const bool hit = (tl.m >> e) & 1u;
-        const unsigned long long bal = __ballot(hit);
-        const int base = __builtin_amdgcn_readlane(off, e);
-        if (hit) {
-            const int pos = base + __popcll(bal & lower);
-            float w = 0.f;
-#pragma unroll
-            for (int k = 0; k < TOPK; ++k) w = (tl.lid[k] == e) ? tl.lw[k] : w;
-            p.sorted_tok[pos] = lane;
-            p.sorted_w[pos] = w;
-            p.tok_slot[(size_t)lane * TOPK + j] = pos;
-            ++j;
-        }
-    }
-    if (valid)
-        for (; j < TOPK; ++j) p.tok_slot[(size_t)lane * TOPK + j] = -1;
-}
-
+// T <= 64: one wave (sort_one_wave: ballots and a shuffle scan, no LDS).
 __global__ __launch_bounds__(64) void sort_small_kernel(Plan p, int bm1, int bm2) {
     sort_one_wave(p, p.topk_ids, p.topk_w, bm1, bm2, threadIdx.x);
 }

@@ -1,0 +1,192 @@
+// One-wave pieces of the local-expert sort, shared by the sort kernels and by
+// the decode GEMM1 kernel that derives its own row tile from the top-k ids.
+//
+// Slot order (solution/triton/kernel.py:460-516 groups a shard's slots by
+// local expert; here the order inside an expert is token-ascending, which
+// makes it deterministic): slot = expert_off[e] + rank of the token among the
+// tokens that picked local expert e.
+#pragma once
+
+#include "common.hpp"
+
+namespace mimoe {
+
+// Largest T the one-wave sort takes (lane t = token t).
+constexpr int SMALL_T = 64;
+
+// A token's local experts: bit mask over the 32 local ids, and per top-k
+// position the local id (-1 if not local) and routing weight.
+struct TokLocal {
+    uint32_t m;
+    int lid[TOPK];
+    float lw[TOPK];
+};
+
+__device__ __forceinline__ TokLocal make_local(const int ids[TOPK], const float ws[TOPK], int off) {
+    TokLocal r;
+    r.m = 0;
+#pragma unroll
+    for (int k = 0; k < TOPK; ++k) {
+        const int l = ids[k] - off;
+        const bool loc = (unsigned)l < (unsigned)EL;
+        r.lid[k] = loc ? l : -1;
+        r.lw[k] = ws[k];
+        r.m |= loc ? (1u << l) : 0u;
+    }
+    return r;
+}
+
+__device__ __forceinline__ TokLocal load_local(const int* ids_base, const float* w_base, int t,
+                                               bool valid, int off) {
+    int ids[TOPK];
+    float ws[TOPK];
+    if (valid) {
+        const int4 i0 = reinterpret_cast<const int4*>(ids_base + (size_t)t * TOPK)[0];
+        const int4 i1 = reinterpret_cast<const int4*>(ids_base + (size_t)t * TOPK)[1];
+        const float4 w0 = reinterpret_cast<const float4*>(w_base + (size_t)t * TOPK)[0];
+        const float4 w1 = reinterpret_cast<const float4*>(w_base + (size_t)t * TOPK)[1];
+        ids[0] = i0.x; ids[1] = i0.y; ids[2] = i0.z; ids[3] = i0.w;
+        ids[4] = i1.x; ids[5] = i1.y; ids[6] = i1.z; ids[7] = i1.w;
+        ws[0] = w0.x; ws[1] = w0.y; ws[2] = w0.z; ws[3] = w0.w;
+        ws[4] = w1.x; ws[5] = w1.y; ws[6] = w1.z; ws[7] = w1.w;
+    } else {
+#pragma unroll
+        for (int k = 0; k < TOPK; ++k) { ids[k] = -1 - EL; ws[k] = 0.f; }  // never local
+    }
+    return make_local(ids, ws, valid ? off : 0);
+}
+
+// Exclusive prefix of the per-expert slot counts held by lanes 0..31 of the
+// calling wave (every lane of the wave must call). Optionally writes the
+// expert offsets and the row-tile prefixes for GEMM tiles of bm1 / bm2 rows.
+__device__ __forceinline__ int scan_counts(const Plan& p, int lane, int c, int bm1, int bm2,
+                                           bool write) {
+    int v0 = c, v1 = (c + bm1 - 1) / bm1, v2 = (c + bm2 - 1) / bm2;
+    const int own0 = v0, own1 = v1, own2 = v2;
+#pragma unroll
+    for (int d = 1; d < EL; d <<= 1) {
+        const int u0 = __shfl_up(v0, d), u1 = __shfl_up(v1, d), u2 = __shfl_up(v2, d);
+        if (lane >= d) { v0 += u0; v1 += u1; v2 += u2; }
+    }
+    if (write && lane < EL) {
+        p.meta[META_EXPERT_OFF + lane] = v0 - own0;
+        p.meta[META_MTILE1 + lane] = v1 - own1;
+        p.meta[META_MTILE2 + lane] = v2 - own2;
+        if (lane == EL - 1) {
+            p.meta[META_EXPERT_OFF + EL] = v0;
+            p.meta[META_MTILE1 + EL] = v1;
+            p.meta[META_MTILE2 + EL] = v2;
+        }
+    }
+    return v0 - own0;
+}
+
+// T <= 64: one wave holds every token (lane t = token t). The expert counts
+// are popcounts of 32 ballots, the offsets a shuffle scan and the placement a
+// second round of ballots: no LDS and no barrier. Writes expert_off, both
+// row-tile prefixes, sorted_tok, sorted_w and tok_slot. UNROLL sets how far
+// the two 32-expert loops unroll: fully in the sort kernels, not at all
+// inside a GEMM kernel, where 32 ballots in flight would spill scalar
+// registers into the GEMM's vector registers.
+template <int UNROLL = EL>
+__device__ inline void sort_one_wave(const Plan& p, const int* ids_base, const float* w_base,
+                                     int bm1, int bm2, int lane) {
+    const bool valid = lane < p.T;
+    const TokLocal tl = load_local(ids_base, w_base, lane, valid, p.local_offset);
+    int cnt = 0;
+#pragma unroll UNROLL
+    for (int e = 0; e < EL; ++e) {
+        const unsigned long long bal = __ballot((tl.m >> e) & 1u);
+        if (lane == e) cnt = __popcll(bal);
+    }
+    const int off = scan_counts(p, lane, cnt, bm1, bm2, true);
+    const unsigned long long lower = (1ull << lane) - 1ull;
+    int j = 0;
+#pragma unroll UNROLL
+    for (int e = 0; e < EL; ++e) {
+        const bool hit = (tl.m >> e) & 1u;
+        const unsigned long long bal = __ballot(hit);
+        const int base = __builtin_amdgcn_readlane(off, e);
+        if (hit) {
+            const int pos = base + __popcll(bal & lower);
+            float w = 0.f;
+#pragma unroll
+            for (int k = 0; k < TOPK; ++k) w = (tl.lid[k] == e) ? tl.lw[k] : w;
+            p.sorted_tok[pos] = lane;
+            p.sorted_w[pos] = w;
+            p.tok_slot[(size_t)lane * TOPK + j] = pos;
+            ++j;
+        }
+    }
+    if (valid)
+        for (; j < TOPK; ++j) p.tok_slot[(size_t)lane * TOPK + j] = -1;
+}
+
+// Position of the k-th set bit (k counted from 0) of a 64-bit mask; k must be
+// below the mask's popcount. Binary search over halves with popcounts.
+__device__ __forceinline__ int nth_set_bit(unsigned long long mask, int k) {
+    int pos = 0;
+#pragma unroll
+    for (int step = 32; step > 0; step >>= 1) {
+        const unsigned long long seg = (mask >> pos) & ((1ull << step) - 1ull);
+        const int c = __popcll(seg);
+        if (k >= c) { k -= c; pos += step; }
+    }
+    return pos;
+}
+
+// Row tile `mt` of bm-row tiles in the slot order of sort_one_wave, found by
+// the calling wave from the top-k ids alone (T <= 64; every lane calls):
+// expert e, first slot row0 = expert_off[e] + rank0, rows, and the mask of
+// tokens (bit t = token t) that picked e. valid is false past the last tile.
+struct WaveTile {
+    int e, row0, nrows, rank0;
+    unsigned long long hits;
+    bool valid;
+};
+
+__device__ __forceinline__ WaveTile wave_tile(const Plan& p, int lane, int mt, int bm) {
+    uint32_t m = 0;
+    if (lane < p.T) {
+        const int4 i0 = reinterpret_cast<const int4*>(p.topk_ids + (size_t)lane * TOPK)[0];
+        const int4 i1 = reinterpret_cast<const int4*>(p.topk_ids + (size_t)lane * TOPK)[1];
+        const int ids[TOPK] = {i0.x, i0.y, i0.z, i0.w, i1.x, i1.y, i1.z, i1.w};
+#pragma unroll
+        for (int k = 0; k < TOPK; ++k) {
+            const int l = ids[k] - p.local_offset;
+            m |= (unsigned)l < (unsigned)EL ? (1u << l) : 0u;
+        }
+    }
+    int cnt = 0;
+#pragma unroll
+    for (int e = 0; e < EL; ++e) {
+        const unsigned long long bal = __ballot((m >> e) & 1u);
+        if (lane == e) cnt = __popcll(bal);
+    }
+    // inclusive prefixes of slots and row tiles over lanes 0..31 (lane = expert)
+    const int tiles = (cnt + bm - 1) / bm;
+    int v0 = cnt, v1 = tiles;
+#pragma unroll
+    for (int d = 1; d < EL; d <<= 1) {
+        const int u0 = __shfl_up(v0, d), u1 = __shfl_up(v1, d);
+        if (lane >= d) { v0 += u0; v1 += u1; }
+    }
+    WaveTile w;
+    w.valid = mt < __builtin_amdgcn_readlane(v1, EL - 1);
+    w.e = w.row0 = w.nrows = w.rank0 = 0;
+    w.hits = 0;
+    if (!w.valid) return w;
+    // experts wholly before tile mt
+    const int ee = __popcll(__ballot(lane < EL && v1 <= mt));
+    const int t0 = __builtin_amdgcn_readlane(v1 - tiles, ee);
+    const int s0 = __builtin_amdgcn_readlane(v0 - cnt, ee);
+    const int ce = __builtin_amdgcn_readlane(cnt, ee);
+    w.e = ee;
+    w.rank0 = (mt - t0) * bm;
+    w.row0 = s0 + w.rank0;
+    w.nrows = min(bm, ce - w.rank0);
+    w.hits = __ballot((m >> ee) & 1u);
+    return w;
+}
+
+}  // namespace mimoe

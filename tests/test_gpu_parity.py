@@ -277,6 +277,49 @@ def test_front_end_fused_and_split_agree(name, fuse, monkeypatch):
     _check_output(wl, out, spread_tokens(wl.T, 64))
 
 
+def _sort_tables(T):
+    """Copies of the sort's tables in the workspace of the last call."""
+    from flashinfer_amd import _lib, kernel
+    L = _lib.workspace_layout(T)
+    ws = kernel.last_workspace()
+    meta = ws[L.expert_off:L.expert_off + 192 * 4].view(torch.int32)
+    S = int(meta[32])
+    return {"expert_off": meta[0:33].clone(), "mtile1": meta[64:97].clone(),
+            "mtile2": meta[128:161].clone(),
+            "sorted_tok": ws[L.sorted_tok:L.sorted_tok + S * 4].view(torch.int32).clone(),
+            "sorted_w": ws[L.sorted_w:L.sorted_w + S * 4].view(torch.int32).clone(),
+            "tok_slot": ws[L.tok_slot:L.tok_slot + T * 32].view(torch.int32).clone()}
+
+
+@pytest.mark.parametrize("T,offset,skew", [(9, 0, False), (16, 96, False), (33, 224, False),
+                                           (64, 0, False), (64, 32, True), (48, 256, False)])
+def test_sort_in_gemm1_matches_sort_launch(T, offset, skew, monkeypatch):
+    """GEMM1 finding its row tiles from the top-k ids (and writing the sort's
+    tables itself) gives bit-identical output and tables to the separate sort
+    launch: ragged T, other shard offsets, four row tiles per expert (skew)
+    and no local token at all (offset 256)."""
+    from flashinfer_amd import _lib, kernel
+    log(f"test_sort_in_gemm1_matches_sort_launch[T={T}-off={offset}-skew={skew}]")
+    wl = W.make_workload("sort_in_gemm1", T, 300 + T, local_expert_offset=offset, skew=skew)
+    monkeypatch.setenv("MI_MOE_SORT_IN_GEMM1", "0")
+    ref = run_gpu(wl, fill=float("nan")).clone()
+    want = _sort_tables(T)
+    # scribble over the tables so the second call must rewrite them
+    L = _lib.workspace_layout(T)
+    ws = kernel.last_workspace()
+    ws[L.expert_off:L.tok_slot + T * 32].fill_(0x5A)
+    monkeypatch.setenv("MI_MOE_SORT_IN_GEMM1", "1")
+    out = run_gpu(wl, fill=float("nan"))
+    got = _sort_tables(T)
+    assert torch.equal(out.view(torch.int16), ref.view(torch.int16))
+    for k in want:
+        assert torch.equal(got[k], want[k]), k
+    if offset == 256:
+        assert int(want["expert_off"][32]) == 0 and bool((out == 0).all())
+    if skew:
+        assert int(want["mtile1"][32]) > int((want["expert_off"][1:] > want["expert_off"][:-1]).sum())
+
+
 def _check_sort_tables(ids, w, offset, got):
     """The sort entry point's tables against the oracle's local assignment."""
     from oracle import ref_moe as R
