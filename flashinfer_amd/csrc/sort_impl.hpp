@@ -81,9 +81,23 @@ __device__ __forceinline__ int scan_counts(const Plan& p, int lane, int c, int b
     return v0 - own0;
 }
 
+// Exclusive prefix sum over the lanes of the wave of x in [0, 128): one
+// ballot per bit plane, counted below the lane with mbcnt (no LDS traffic).
+__device__ __forceinline__ int excl_prefix_small(int x) {
+    int s = 0;
+#pragma unroll
+    for (int k = 0; k < 7; ++k) {
+        const unsigned long long b = __ballot((x >> k) & 1);
+        const uint32_t below = __builtin_amdgcn_mbcnt_hi(
+            (uint32_t)(b >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)b, 0u));
+        s += (int)below << k;
+    }
+    return s;
+}
+
 // T <= 64: one wave holds every token (lane t = token t). The expert counts
-// are popcounts of 32 ballots, the offsets a shuffle scan and the placement a
-// second round of ballots: no LDS and no barrier. Writes expert_off, both
+// are popcounts of 32 ballots, the offsets bit-plane prefixes and the
+// placement a second round of ballots: no LDS and no barrier. Writes expert_off, both
 // row-tile prefixes, sorted_tok, sorted_w and tok_slot. UNROLL sets how far
 // the two 32-expert loops unroll: fully in the sort kernels, not at all
 // inside a GEMM kernel, where 32 ballots in flight would spill scalar
@@ -99,7 +113,20 @@ __device__ inline void sort_one_wave(const Plan& p, const int* ids_base, const f
         const unsigned long long bal = __ballot((tl.m >> e) & 1u);
         if (lane == e) cnt = __popcll(bal);
     }
-    const int off = scan_counts(p, lane, cnt, bm1, bm2, true);
+    // offsets and both row-tile prefixes (counts <= 64: bit-plane prefixes)
+    const int t1 = (cnt + bm1 - 1) / bm1, t2 = (cnt + bm2 - 1) / bm2;
+    const int off = excl_prefix_small(cnt);
+    const int o1 = excl_prefix_small(t1), o2 = excl_prefix_small(t2);
+    if (lane < EL) {
+        p.meta[META_EXPERT_OFF + lane] = off;
+        p.meta[META_MTILE1 + lane] = o1;
+        p.meta[META_MTILE2 + lane] = o2;
+        if (lane == EL - 1) {
+            p.meta[META_EXPERT_OFF + EL] = off + cnt;
+            p.meta[META_MTILE1 + EL] = o1 + t1;
+            p.meta[META_MTILE2 + EL] = o2 + t2;
+        }
+    }
     const unsigned long long lower = (1ull << lane) - 1ull;
     int j = 0;
 #pragma unroll UNROLL
@@ -165,12 +192,8 @@ __device__ __forceinline__ WaveTile wave_tile(const Plan& p, int lane, int mt, i
     }
     // inclusive prefixes of slots and row tiles over lanes 0..31 (lane = expert)
     const int tiles = (cnt + bm - 1) / bm;
-    int v0 = cnt, v1 = tiles;
-#pragma unroll
-    for (int d = 1; d < EL; d <<= 1) {
-        const int u0 = __shfl_up(v0, d), u1 = __shfl_up(v1, d);
-        if (lane >= d) { v0 += u0; v1 += u1; }
-    }
+    const int v0 = excl_prefix_small(cnt) + cnt;
+    const int v1 = excl_prefix_small(tiles) + tiles;
     WaveTile w;
     w.valid = mt < __builtin_amdgcn_readlane(v1, EL - 1);
     w.e = w.row0 = w.nrows = w.rank0 = 0;
