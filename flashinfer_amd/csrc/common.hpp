@@ -145,12 +145,13 @@ hipError_t launch_route_sort(const Plan& p, const float* logits, const void* bia
                              int bm1, int bm2, hipStream_t s);
 hipError_t launch_gemm1(const Plan& p, const uint8_t* hs, const float* hs_scale, const uint8_t* w1,
                         const float* w1s, int variant, hipStream_t s);
-// GEMM1 variant 16 that also does the sort's work (T <= 64): reads the top-k
-// ids instead of the sort's tables and writes those tables (bm1 / bm2 tile
-// prefixes) for the kernels after it, so no sort launch precedes it.
+// GEMM1 stream variants 16 and 5 that also do the sort's work (T <= 64):
+// they read the top-k ids instead of the sort's tables and write those tables
+// (bm1 / bm2 tile prefixes) for the kernels after them, so no sort launch
+// precedes them.
 bool gemm1_sorts_supported(int T, int variant);
 hipError_t launch_gemm1_sorting(const Plan& p, const uint8_t* hs, const float* hs_scale,
-                                const uint8_t* w1, const float* w1s, int bm1, int bm2,
+                                const uint8_t* w1, const float* w1s, int variant, int bm1, int bm2,
                                 hipStream_t s);
 hipError_t launch_gemm2(const Plan& p, const uint8_t* w2, const float* w2s, int variant,
                         hipStream_t s);

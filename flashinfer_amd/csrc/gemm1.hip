@@ -34,7 +34,7 @@
 namespace mimoe {
 
 template <int MT, int D, int NW, int KS = 1, bool SORT = false>
-__global__ __launch_bounds__(64 * NW * KS) __attribute__((amdgpu_waves_per_eu(SORT ? 5 : 1)))
+__global__ __launch_bounds__(64 * NW * KS) __attribute__((amdgpu_waves_per_eu(SORT && KS == 4 ? 5 : 1)))
 void gemm1_stream_kernel(Plan p, const uint8_t* __restrict__ hs,
                                                                     const float* __restrict__ hs_scale,
                                                                     const uint8_t* __restrict__ w1,
@@ -207,13 +207,18 @@ static void launch_stream1(const Plan& p, const uint8_t* hs, const float* hs_sca
                        hs, hs_scale, w1, w1s, bm1, bm2);
 }
 
-bool gemm1_sorts_supported(int T, int variant) { return variant == 16 && T > 0 && T <= SMALL_T; }
+bool gemm1_sorts_supported(int T, int variant) {
+    return (variant == 16 || variant == 5) && T > 0 && T <= SMALL_T;
+}
 
 hipError_t launch_gemm1_sorting(const Plan& p, const uint8_t* hs, const float* hs_scale,
-                                const uint8_t* w1, const float* w1s, int bm1, int bm2,
+                                const uint8_t* w1, const float* w1s, int variant, int bm1, int bm2,
                                 hipStream_t s) {
     if (p.T <= 0) return hipSuccess;
-    launch_stream1<1, 2, 1, 4, true>(p, hs, hs_scale, w1, w1s, s, bm1, bm2);
+    if (variant == 5)
+        launch_stream1<1, 4, 1, 1, true>(p, hs, hs_scale, w1, w1s, s, bm1, bm2);
+    else
+        launch_stream1<1, 2, 1, 4, true>(p, hs, hs_scale, w1, w1s, s, bm1, bm2);
     return hipGetLastError();
 }
 
