@@ -185,6 +185,35 @@ def test_skew_all_rows_on_biased_experts():
     assert torch.equal(eoff, want)
 
 
+def _random_configs(n=20, seed=2026):
+    """Seeded (T, offset, skew, routed_scaling_factor) draws: ragged T from 1
+    to ~1100 (weighted to decode sizes), shard offsets that are negative,
+    unaligned or near the end of the 256 experts."""
+    g = torch.Generator().manual_seed(seed)
+    pick = lambda xs: xs[int(torch.randint(len(xs), (1,), generator=g))]
+    out = []
+    for i in range(n):
+        band = pick([(1, 8), (9, 64), (9, 64), (65, 300), (1000, 1100)])
+        T = int(torch.randint(band[0], band[1] + 1, (1,), generator=g))
+        offset = pick([-40, -8, 0, 5, 32, 100, 200, 224, 250])
+        skew = offset >= 0 and offset <= 248 and bool(torch.rand(1, generator=g) < 0.25)
+        out.append((i, T, offset, skew, pick([1.0, 2.5])))
+    return out
+
+
+@pytest.mark.parametrize("i,T,offset,skew,rsf", _random_configs())
+def test_random_configs(i, T, offset, skew, rsf):
+    """Output against the oracle on seeded random shapes and shard offsets
+    through the default kernel choice for each T."""
+    log(f"test_random_configs[{i}: T={T} off={offset} skew={skew} rsf={rsf}]")
+    wl = W.make_workload(f"random_{i}", T, 5000 + i, local_expert_offset=offset, skew=skew,
+                         routed_scaling_factor=rsf)
+    _route_check(wl)
+    out = run_gpu(wl, fill=float("nan"))
+    assert torch.isfinite(out.float()).all()
+    _check_output(wl, out, spread_tokens(T, 40))
+
+
 # Both sides of every T at which the default kernels change: fused GEMM2+combine
 # and fused route+sort (T <= 4), sort inside GEMM1 (T <= 64), streaming GEMM
 # shapes (32, 128), wide GEMM1 (> 128), wide GEMM2 (193..256), tiled GEMM2
