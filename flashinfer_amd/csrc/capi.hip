@@ -5,8 +5,9 @@
 // nothing and reports why through mi_moe_last_error(). The call enqueues
 // route -> sort -> GEMM1+SwiGLU -> GEMM2 -> combine on the caller's stream
 // with grids sized from T alone: no device-to-host copy, no host sync
-// (the reference syncs three times, kernel.py:572, :718, :773). Small T folds
-// route and sort into one launch (T <= 4) or the sort into GEMM1 (T <= 64).
+// (the reference syncs three times, kernel.py:572, :718, :773). At decode
+// sizes routing and the sort fold into GEMM1 (T = 1), into one launch
+// (T <= 4), or the sort alone folds into GEMM1 (T <= 64); see pick_front.
 #include <math.h>
 #include <stdarg.h>
 #include <stdio.h>
@@ -88,24 +89,41 @@ struct Variants {
     int g1, g2;
 };
 
-// Routing and sort as one launch for small T (MI_MOE_FUSE_FRONT=0/1 overrides).
-// From T = 5 routing as its own launch plus the sort inside GEMM1 is faster
-// (measured 2-3 us per call at T = 5..8); at T <= 4 the two are level.
-bool fuse_front_end(int64_t T) {
-    bool f = T <= 4;
-    const char* env = getenv("MI_MOE_FUSE_FRONT");
-    if (env && *env) f = atoi(env) != 0;
-    return f && route_sort_supported((int)T);
+// Which launches do routing and the sort (decode sizes fold them into
+// others). MI_MOE_FUSE_FRONT, MI_MOE_ROUTE_IN_GEMM1 and MI_MOE_SORT_IN_GEMM1
+// (=0/1) override the defaults, in that order of precedence.
+enum class Front {
+    KERNELS,         // routing kernel, sort kernel(s)
+    FUSED,           // one single-workgroup routing + sort kernel
+    SORT_IN_GEMM1,   // routing kernel; GEMM1 sorts (FRONT_SORT)
+    ROUTE_IN_GEMM1,  // GEMM1 routes and sorts (FRONT_ROUTE)
+};
+
+// Largest T whose routing every GEMM1 workgroup repeats by default. Each
+// workgroup routes all T tokens before its first weight load, which costs
+// more than the routing launch it saves from T = 2 on (measured per call:
+// T=1 18.9 against 21.7 us, T=2 27.9 against 27.1, T=4 43.9 against 38.6,
+// T=16 119.6 against 89.0).
+constexpr int64_t ROUTE_IN_GEMM1_MAX_T = 1;
+
+int env_flag(const char* name) {  // -1 unset, else 0 / 1
+    const char* v = getenv(name);
+    return (v && *v) ? (atoi(v) != 0) : -1;
 }
 
-// GEMM1 does the sort's work itself (no sort launch) where it can: the
-// K-split stream variant at T <= 64 without the fused front end
-// (MI_MOE_SORT_IN_GEMM1=0/1 overrides).
-bool sort_in_gemm1(int64_t T, int g1) {
-    bool f = true;
-    const char* env = getenv("MI_MOE_SORT_IN_GEMM1");
-    if (env && *env) f = atoi(env) != 0;
-    return f && !fuse_front_end(T) && gemm1_sorts_supported((int)T, g1);
+Front pick_front(int64_t T, int g1) {
+    const int fuse = env_flag("MI_MOE_FUSE_FRONT");
+    const int route = env_flag("MI_MOE_ROUTE_IN_GEMM1");
+    const int sort = env_flag("MI_MOE_SORT_IN_GEMM1");
+    const bool g1_can = gemm1_sorts_supported((int)T, g1);
+    const bool fused_ok = route_sort_supported((int)T);
+    if (fuse == 1 && fused_ok) return Front::FUSED;
+    if (g1_can && (route == -1 ? T <= ROUTE_IN_GEMM1_MAX_T : route == 1)) return Front::ROUTE_IN_GEMM1;
+    // From T = 5 routing as its own launch plus the sort inside GEMM1 beats
+    // the fused routing + sort kernel (measured 2-3 us per call at T = 5..8).
+    if (fuse == -1 && T <= 4 && fused_ok) return Front::FUSED;
+    if (g1_can && sort != 0) return Front::SORT_IN_GEMM1;
+    return Front::KERNELS;
 }
 
 Variants pick_variants(int64_t T) {
@@ -284,27 +302,28 @@ static int run_impl(const mi_moe_args* a, hipStream_t s, hipEvent_t const* ev) {
         if (ev && err == hipSuccess) err = hipEventRecord(ev[i], s);
     };
     const int bias_f32 = a->bias_dtype == MI_MOE_DTYPE_F32;
-    const bool g1_sorts = sort_in_gemm1(T, var.g1);
+    const Front front = pick_front(T, var.g1);
+    const FrontArgs fa{a->routing_logits, a->routing_bias, bias_f32, gemm1_bm(var.g1),
+                       gemm2_bm(var.g2)};
     mark(0);
-    if (fuse_front_end(T)) {
+    if (front == Front::FUSED) {
         if (err == hipSuccess)
-            err = launch_route_sort(p, a->routing_logits, a->routing_bias, bias_f32,
-                                    gemm1_bm(var.g1), gemm2_bm(var.g2), s);
-        mark(1);
-    } else {
+            err = launch_route_sort(p, a->routing_logits, a->routing_bias, bias_f32, fa.bm1, fa.bm2,
+                                    s);
+    } else if (front != Front::ROUTE_IN_GEMM1) {
         if (err == hipSuccess)
             err = launch_route(a->routing_logits, a->routing_bias, bias_f32, p.T, p.rsf,
                                p.topk_ids, p.topk_w, s);
-        mark(1);
-        if (err == hipSuccess && !g1_sorts)
-            err = launch_sort(p, gemm1_bm(var.g1), gemm2_bm(var.g2), s);
     }
+    mark(1);
+    if (err == hipSuccess && front == Front::KERNELS) err = launch_sort(p, fa.bm1, fa.bm2, s);
     mark(2);
     if (err == hipSuccess) {
-        if (g1_sorts)
-            err = launch_gemm1_sorting(p, a->hidden_states, a->hidden_states_scale,
-                                       a->gemm1_weights, a->gemm1_weights_scale, var.g1,
-                                       gemm1_bm(var.g1), gemm2_bm(var.g2), s);
+        if (front == Front::SORT_IN_GEMM1 || front == Front::ROUTE_IN_GEMM1)
+            err = launch_gemm1_front(p, a->hidden_states, a->hidden_states_scale, a->gemm1_weights,
+                                     a->gemm1_weights_scale, var.g1,
+                                     front == Front::ROUTE_IN_GEMM1 ? FRONT_ROUTE : FRONT_SORT, fa,
+                                     s);
         else
             err = launch_gemm1(p, a->hidden_states, a->hidden_states_scale, a->gemm1_weights,
                                a->gemm1_weights_scale, var.g1, s);

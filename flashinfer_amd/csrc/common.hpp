@@ -127,9 +127,10 @@ __device__ __forceinline__ bool find_tile(const int* meta, int mtile_base, int m
 }
 
 // Upper bound on the row tiles of all experts: sum_e ceil(c_e / bm) with
-// sum_e c_e <= 8T and c_e <= T.
+// sum_e c_e <= 8T, c_e <= T and at most min(32, 8T) experts holding slots
+// (each adds under one tile of rounding).
 inline int max_mtiles(int T, int bm) {
-    const long long a = (8LL * T + bm - 1) / bm + EL;
+    const long long a = (8LL * T + bm - 1) / bm + (8LL * T < EL ? 8LL * T : EL);
     const long long b = (long long)EL * ((T + bm - 1) / bm);
     return (int)(a < b ? a : b);
 }
@@ -145,14 +146,26 @@ hipError_t launch_route_sort(const Plan& p, const float* logits, const void* bia
                              int bm1, int bm2, hipStream_t s);
 hipError_t launch_gemm1(const Plan& p, const uint8_t* hs, const float* hs_scale, const uint8_t* w1,
                         const float* w1s, int variant, hipStream_t s);
-// GEMM1 stream variants 16 and 5 that also do the sort's work (T <= 64):
-// they read the top-k ids instead of the sort's tables and write those tables
-// (bm1 / bm2 tile prefixes) for the kernels after them, so no sort launch
-// precedes them.
+// Front-end work a GEMM1 stream kernel can do itself at decode sizes: none
+// (it reads the sort's tables), the sort (from the top-k ids in the
+// workspace), or routing and the sort (from the logits).
+constexpr int FRONT_NONE = 0;
+constexpr int FRONT_SORT = 1;
+constexpr int FRONT_ROUTE = 2;
+struct FrontArgs {
+    const float* logits;  // [T, 256] (FRONT_ROUTE)
+    const void* bias;     // [256] bf16 or fp32 (FRONT_ROUTE)
+    int bias_is_f32;
+    int bm1, bm2;         // row-tile heights of the GEMM1 / GEMM2 kernels for the tables
+};
+// GEMM1 stream variants 16 and 5 with FRONT_SORT or FRONT_ROUTE (T <= 64):
+// they find their row tiles themselves and write the sort's tables (and, with
+// FRONT_ROUTE, the top-k) for the kernels after them, so no sort (or routing)
+// launch precedes them.
 bool gemm1_sorts_supported(int T, int variant);
-hipError_t launch_gemm1_sorting(const Plan& p, const uint8_t* hs, const float* hs_scale,
-                                const uint8_t* w1, const float* w1s, int variant, int bm1, int bm2,
-                                hipStream_t s);
+hipError_t launch_gemm1_front(const Plan& p, const uint8_t* hs, const float* hs_scale,
+                              const uint8_t* w1, const float* w1s, int variant, int front,
+                              const FrontArgs& fa, hipStream_t s);
 hipError_t launch_gemm2(const Plan& p, const uint8_t* w2, const float* w2s, int variant,
                         hipStream_t s);
 hipError_t launch_combine(const Plan& p, uint16_t* out, hipStream_t s);

@@ -23,30 +23,37 @@
 // A and B use the same mapping, so the k pairing inside the MFMA is exact
 // whatever order the instruction assigns to the 32 bytes of a lane.
 //
-// With SORT (T <= 64, MT = 1) the kernel also stands in for the sort launch:
-// each wave derives its row tile and its rows' tokens from the top-k ids
-// (wave_tile: the one-wave sort's counts and scan, in registers), so no
+// With FRONT_SORT (T <= 64, MT = 1) the kernel also stands in for the sort
+// launch: each wave derives its row tile and its rows' tokens from the top-k
+// ids (wave_tile: the one-wave sort's counts and scan, in registers), so no
 // kernel boundary separates routing from GEMM1, and workgroup (0, 0) writes
 // the sort's tables (expert offsets, tile prefixes for bm1 / bm2, slot lists)
-// for GEMM2 and the combine, which run after this kernel.
+// for GEMM2 and the combine, which run after this kernel. With FRONT_ROUTE
+// every workgroup first routes all T tokens itself (its waves take them
+// round-robin, route_token as in the routing kernel) into LDS, and
+// workgroup (0, 0) also writes the top-k: the call then starts with GEMM1.
+#include "route_impl.hpp"
 #include "sort_impl.hpp"
 
 namespace mimoe {
 
-template <int MT, int D, int NW, int KS = 1, bool SORT = false>
-__global__ __launch_bounds__(64 * NW * KS) __attribute__((amdgpu_waves_per_eu(SORT && KS == 4 ? 5 : 1)))
-void gemm1_stream_kernel(Plan p, const uint8_t* __restrict__ hs,
-                                                                    const float* __restrict__ hs_scale,
-                                                                    const uint8_t* __restrict__ w1,
-                                                                    const float* __restrict__ w1s,
-                                                                    int bm1, int bm2) {
+template <int MT, int D, int NW, int KS = 1, int FRONT = FRONT_NONE>
+__global__ __launch_bounds__(64 * NW * KS)
+__attribute__((amdgpu_waves_per_eu(FRONT != FRONT_NONE && KS == 4 ? 5 : 1)))
+void gemm1_stream_kernel(Plan p, const uint8_t* __restrict__ hs, const float* __restrict__ hs_scale,
+                         const uint8_t* __restrict__ w1, const float* __restrict__ w1s, FrontArgs fa) {
     constexpr int KB = HB / KS;  // k-blocks per wave
+    constexpr int NWAVES = NW * KS;
     static_assert(HB % KS == 0 && KB % D == 0, "k split and prefetch depth must divide the k-blocks");
-    static_assert(!SORT || MT == 1, "the in-kernel sort gives each lane the token of one row");
+    static_assert(FRONT == FRONT_NONE || MT == 1, "the in-kernel sort gives each lane the token of one row");
     constexpr int BM = 16 * MT;
     __shared__ float sa_lds[HB][BM];
     // partial sums of waves 1..KS-1 of a column group: [split-1][group][value][lane]
     __shared__ float red[KS > 1 ? KS - 1 : 1][NW][KS > 1 ? 8 * MT : 1][64];
+    // top-k of every token, routed in this workgroup (FRONT_ROUTE, T <= 64)
+    constexpr int RT = FRONT == FRONT_ROUTE ? SMALL_T * TOPK : 4;
+    __shared__ __attribute__((aligned(16))) int s_ids[RT];
+    __shared__ __attribute__((aligned(16))) float s_w[RT];
 
     const int tid = threadIdx.x;
     const int lane = tid & 63;
@@ -56,10 +63,39 @@ void gemm1_stream_kernel(Plan p, const uint8_t* __restrict__ hs,
     // Row tile and the tokens of this lane's rows (row i * 16 + r).
     int e, row0, nrows;
     int tok[MT];
-    if constexpr (SORT) {
-        const WaveTile wt = wave_tile(p, lane, blockIdx.y, BM);
-        if (blockIdx.x == 0 && blockIdx.y == 0 && wave == 0)
-            sort_one_wave<1>(p, p.topk_ids, p.topk_w, bm1, bm2, lane);
+    if constexpr (FRONT != FRONT_NONE) {
+        const int* ids_src = p.topk_ids;
+        const float* w_src = p.topk_w;
+        if constexpr (FRONT == FRONT_ROUTE) {
+            for (int t = wave; t < p.T; t += NWAVES) {
+                int ids[TOPK];
+                float w[TOPK];
+                route_token(fa.logits + (size_t)t * EG, fa.bias, fa.bias_is_f32, p.rsf, lane, ids, w);
+                if (lane == 0) {
+                    reinterpret_cast<int4*>(s_ids + t * TOPK)[0] = make_int4(ids[0], ids[1], ids[2], ids[3]);
+                    reinterpret_cast<int4*>(s_ids + t * TOPK)[1] = make_int4(ids[4], ids[5], ids[6], ids[7]);
+                    reinterpret_cast<float4*>(s_w + t * TOPK)[0] = make_float4(w[0], w[1], w[2], w[3]);
+                    reinterpret_cast<float4*>(s_w + t * TOPK)[1] = make_float4(w[4], w[5], w[6], w[7]);
+                }
+            }
+            __syncthreads();
+            ids_src = s_ids;
+            w_src = s_w;
+        }
+        const WaveTile wt = wave_tile(p, ids_src, lane, blockIdx.y, BM);
+        if (blockIdx.x == 0 && blockIdx.y == 0 && wave == 0) {
+            if constexpr (FRONT == FRONT_ROUTE) {
+                if (lane < p.T) {  // the global top-k, as the routing kernel writes it
+                    int4* io = reinterpret_cast<int4*>(p.topk_ids + (size_t)lane * TOPK);
+                    float4* wo = reinterpret_cast<float4*>(p.topk_w + (size_t)lane * TOPK);
+                    io[0] = reinterpret_cast<const int4*>(s_ids + lane * TOPK)[0];
+                    io[1] = reinterpret_cast<const int4*>(s_ids + lane * TOPK)[1];
+                    wo[0] = reinterpret_cast<const float4*>(s_w + lane * TOPK)[0];
+                    wo[1] = reinterpret_cast<const float4*>(s_w + lane * TOPK)[1];
+                }
+            }
+            sort_one_wave<1>(p, ids_src, w_src, fa.bm1, fa.bm2, lane);
+        }
         if (!wt.valid) return;  // the same for every wave of the workgroup
         e = wt.e;
         row0 = wt.row0;
@@ -198,27 +234,31 @@ int gemm1_bm(int variant) {
     }
 }
 
-template <int MT, int D, int NW, int KS = 1, bool SORT = false>
+template <int MT, int D, int NW, int KS = 1, int FRONT = FRONT_NONE>
 static void launch_stream1(const Plan& p, const uint8_t* hs, const float* hs_scale,
-                           const uint8_t* w1, const float* w1s, hipStream_t s, int bm1 = 0,
-                           int bm2 = 0) {
+                           const uint8_t* w1, const float* w1s, hipStream_t s,
+                           const FrontArgs& fa = FrontArgs{}) {
     dim3 grid(I / (16 * NW), max_mtiles(p.T, 16 * MT));
-    hipLaunchKernelGGL((gemm1_stream_kernel<MT, D, NW, KS, SORT>), grid, dim3(64 * NW * KS), 0, s, p,
-                       hs, hs_scale, w1, w1s, bm1, bm2);
+    hipLaunchKernelGGL((gemm1_stream_kernel<MT, D, NW, KS, FRONT>), grid, dim3(64 * NW * KS), 0, s,
+                       p, hs, hs_scale, w1, w1s, fa);
 }
 
 bool gemm1_sorts_supported(int T, int variant) {
     return (variant == 16 || variant == 5) && T > 0 && T <= SMALL_T;
 }
 
-hipError_t launch_gemm1_sorting(const Plan& p, const uint8_t* hs, const float* hs_scale,
-                                const uint8_t* w1, const float* w1s, int variant, int bm1, int bm2,
-                                hipStream_t s) {
+hipError_t launch_gemm1_front(const Plan& p, const uint8_t* hs, const float* hs_scale,
+                              const uint8_t* w1, const float* w1s, int variant, int front,
+                              const FrontArgs& fa, hipStream_t s) {
     if (p.T <= 0) return hipSuccess;
-    if (variant == 5)
-        launch_stream1<1, 4, 1, 1, true>(p, hs, hs_scale, w1, w1s, s, bm1, bm2);
-    else
-        launch_stream1<1, 2, 1, 4, true>(p, hs, hs_scale, w1, w1s, s, bm1, bm2);
+    if (!gemm1_sorts_supported(p.T, variant)) return hipErrorInvalidValue;
+    if (front == FRONT_ROUTE) {
+        if (variant == 5) launch_stream1<1, 4, 1, 1, FRONT_ROUTE>(p, hs, hs_scale, w1, w1s, s, fa);
+        else launch_stream1<1, 2, 1, 4, FRONT_ROUTE>(p, hs, hs_scale, w1, w1s, s, fa);
+    } else {
+        if (variant == 5) launch_stream1<1, 4, 1, 1, FRONT_SORT>(p, hs, hs_scale, w1, w1s, s, fa);
+        else launch_stream1<1, 2, 1, 4, FRONT_SORT>(p, hs, hs_scale, w1, w1s, s, fa);
+    }
     return hipGetLastError();
 }
 

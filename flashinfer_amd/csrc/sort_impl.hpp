@@ -163,7 +163,8 @@ __device__ __forceinline__ int nth_set_bit(unsigned long long mask, int k) {
 }
 
 // Row tile `mt` of bm-row tiles in the slot order of sort_one_wave, found by
-// the calling wave from the top-k ids alone (T <= 64; every lane calls):
+// the calling wave from the top-k ids alone (ids_base: [T, 8], global or
+// LDS; T <= 64; every lane calls):
 // expert e, first slot row0 = expert_off[e] + rank0, rows, and the mask of
 // tokens (bit t = token t) that picked e. valid is false past the last tile.
 struct WaveTile {
@@ -172,11 +173,12 @@ struct WaveTile {
     bool valid;
 };
 
-__device__ __forceinline__ WaveTile wave_tile(const Plan& p, int lane, int mt, int bm) {
+__device__ __forceinline__ WaveTile wave_tile(const Plan& p, const int* ids_base, int lane, int mt,
+                                              int bm) {
     uint32_t m = 0;
     if (lane < p.T) {
-        const int4 i0 = reinterpret_cast<const int4*>(p.topk_ids + (size_t)lane * TOPK)[0];
-        const int4 i1 = reinterpret_cast<const int4*>(p.topk_ids + (size_t)lane * TOPK)[1];
+        const int4 i0 = reinterpret_cast<const int4*>(ids_base + (size_t)lane * TOPK)[0];
+        const int4 i1 = reinterpret_cast<const int4*>(ids_base + (size_t)lane * TOPK)[1];
         const int ids[TOPK] = {i0.x, i0.y, i0.z, i0.w, i1.x, i1.y, i1.z, i1.w};
 #pragma unroll
         for (int k = 0; k < TOPK; ++k) {

@@ -333,6 +333,7 @@ def test_sort_in_gemm1_matches_sort_launch(T, offset, skew, monkeypatch):
     log(f"test_sort_in_gemm1_matches_sort_launch[T={T}-off={offset}-skew={skew}]")
     wl = W.make_workload("sort_in_gemm1", T, 300 + T, local_expert_offset=offset, skew=skew)
     monkeypatch.setenv("MI_MOE_FUSE_FRONT", "0")
+    monkeypatch.setenv("MI_MOE_ROUTE_IN_GEMM1", "0")
     monkeypatch.setenv("MI_MOE_SORT_IN_GEMM1", "0")
     ref = run_gpu(wl, fill=float("nan")).clone()
     want = _sort_tables(T)
@@ -350,6 +351,42 @@ def test_sort_in_gemm1_matches_sort_launch(T, offset, skew, monkeypatch):
         assert int(want["expert_off"][32]) == 0 and bool((out == 0).all())
     if skew and T > 16:  # some expert spans several 16-row tiles
         assert int(want["mtile1"][32]) > int((want["expert_off"][1:] > want["expert_off"][:-1]).sum())
+
+
+@pytest.mark.parametrize("T,offset,skew,force", [(1, 0, False, False), (2, 32, True, False),
+                                                 (4, 96, False, False), (7, 0, False, False),
+                                                 (16, 224, False, False), (16, 32, True, False),
+                                                 (12, 256, False, False), (33, 0, False, True),
+                                                 (64, 32, True, True)])
+def test_route_in_gemm1_matches_separate_launches(T, offset, skew, force, monkeypatch):
+    """GEMM1 routing every token itself (each workgroup, into LDS), sorting,
+    and writing the top-k and the sort tables gives bit-identical output,
+    top-k and tables to the routing and sort kernels: both GEMM1 shapes
+    (single-wave workgroups at T <= 4, K split above), T up to 64 when forced
+    on, other shard offsets, skewed routing and no local token."""
+    from flashinfer_amd import _lib, kernel
+    log(f"test_route_in_gemm1_matches_separate_launches[T={T}-off={offset}-skew={skew}]")
+    wl = W.make_workload("route_in_gemm1", T, 400 + T, local_expert_offset=offset, skew=skew)
+    for k in ("MI_MOE_FUSE_FRONT", "MI_MOE_ROUTE_IN_GEMM1", "MI_MOE_SORT_IN_GEMM1"):
+        monkeypatch.setenv(k, "0")
+    ref = run_gpu(wl, fill=float("nan")).clone()
+    want = _sort_tables(T)
+    L = _lib.workspace_layout(T)
+    ws = kernel.last_workspace()
+    topk_want = ws[L.topk_ids:L.expert_off].clone()
+    ws[L.topk_ids:L.tok_slot + T * 32].fill_(0x5A)
+    if force:
+        monkeypatch.setenv("MI_MOE_ROUTE_IN_GEMM1", "1")
+    else:
+        for k in ("MI_MOE_FUSE_FRONT", "MI_MOE_ROUTE_IN_GEMM1", "MI_MOE_SORT_IN_GEMM1"):
+            monkeypatch.delenv(k)
+    out = run_gpu(wl, fill=float("nan"))
+    got = _sort_tables(T)
+    assert torch.equal(out.view(torch.int16), ref.view(torch.int16))
+    assert torch.equal(ws[L.topk_ids:L.topk_ids + T * 32], topk_want[:T * 32])
+    assert torch.equal(ws[L.topk_w:L.topk_w + T * 32], topk_want[L.topk_w - L.topk_ids:][:T * 32])
+    for k in want:
+        assert torch.equal(got[k], want[k]), k
 
 
 def _check_sort_tables(ids, w, offset, got):
