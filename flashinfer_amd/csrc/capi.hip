@@ -6,8 +6,8 @@
 // route -> sort -> GEMM1+SwiGLU -> GEMM2 -> combine on the caller's stream
 // with grids sized from T alone: no device-to-host copy, no host sync
 // (the reference syncs three times, kernel.py:572, :718, :773). At decode
-// sizes routing and the sort fold into GEMM1 (T = 1), into one launch
-// (T <= 4), or the sort alone folds into GEMM1 (T <= 64); see pick_front.
+// sizes routing and the sort fold into GEMM1 (T = 1), or the sort alone does
+// (T <= 64); see pick_front.
 #include <math.h>
 #include <stdarg.h>
 #include <stdio.h>
@@ -119,9 +119,11 @@ Front pick_front(int64_t T, int g1) {
     const bool fused_ok = route_sort_supported((int)T);
     if (fuse == 1 && fused_ok) return Front::FUSED;
     if (g1_can && (route == -1 ? T <= ROUTE_IN_GEMM1_MAX_T : route == 1)) return Front::ROUTE_IN_GEMM1;
-    // From T = 5 routing as its own launch plus the sort inside GEMM1 beats
-    // the fused routing + sort kernel (measured 2-3 us per call at T = 5..8).
-    if (fuse == -1 && T <= 4 && fused_ok) return Front::FUSED;
+    // Routing as its own launch plus the sort inside the K-split GEMM1 beats
+    // the fused routing + sort kernel from T = 2 when the shard has slots
+    // (measured per call, four seeds at T = 3..4: 1.5-4 us; T = 5..8: 2-3 us;
+    // 2.5 us slower only when no token is local), so the fused kernel runs
+    // only when asked for.
     if (g1_can && sort != 0) return Front::SORT_IN_GEMM1;
     return Front::KERNELS;
 }
@@ -132,7 +134,9 @@ Variants pick_variants(int64_t T) {
     // waves) while an expert has at most a few row tiles, 64-column GEMM2 waves from T = 64, the
     // wide kernels (register-ring weights, LDS activations) for roughly 5 to
     // 70 rows per expert (GEMM2 from ~10 to ~15), the LDS-tiled kernels beyond.
-    if (T <= 4) v = {5, VARIANT_GEMM2_COMBINE};  // one launch fewer where launches dominate
+    // GEMM2 with the combine in one launch fewer where launches dominate
+    if (T <= 1) v = {5, VARIANT_GEMM2_COMBINE};
+    else if (T <= 4) v = {16, VARIANT_GEMM2_COMBINE};
     else if (T <= 32) v = {16, 5};
     else if (T <= 128) v = {16, 14};
     else if (T <= 192) v = {15, 13};

@@ -91,9 +91,8 @@ int mi_moe_run(const mi_moe_args* args, void* stream);
  * (hipEvent_t, n_events == MI_MOE_NUM_PHASES + 1) on the stream before the
  * first kernel and after each of the phases route, sort, gemm1 (+SwiGLU),
  * gemm2, combine. A phase whose work another launch does (routing and the
- * sort inside GEMM1 at T = 1, the sort inside routing at T <= 4 or inside
- * GEMM1 up to T = 64, the combine inside GEMM2 at T <= 4) records its two
- * events back to back. Counterpart of the
+ * sort inside GEMM1 at T = 1, the sort inside GEMM1 up to T = 64, the combine
+ * inside GEMM2 at T <= 4) records its two events back to back. Counterpart of the
  * reference's env-gated phase events (kernel.py:634-672, phase names
  * :677-823). */
 #define MI_MOE_NUM_PHASES 5

@@ -215,10 +215,10 @@ def test_random_configs(i, T, offset, skew, rsf):
 
 
 # Both sides of every T at which the default kernels change: fused GEMM2+combine
-# and fused route+sort (T <= 4), sort inside GEMM1 (T <= 64), streaming GEMM
+# (T <= 4), routing inside GEMM1 (T = 1), sort inside GEMM1 (T <= 64), streaming GEMM
 # shapes (32, 128), wide GEMM1 (> 128), wide GEMM2 (193..256), tiled GEMM2
 # (> 256), chunked two-kernel sort (> 1024), LDS-tiled GEMM1 (> 1536).
-@pytest.mark.parametrize("T", [2, 4, 5, 8, 9, 32, 33, 64, 65, 128, 129, 192, 193, 256, 257, 1024,
+@pytest.mark.parametrize("T", [1, 2, 4, 5, 8, 9, 32, 33, 64, 65, 128, 129, 192, 193, 256, 257, 1024,
                                1025, 1536, 1537, 2049])
 def test_variant_boundaries(T):
     log(f"test_variant_boundaries[T={T}]")
@@ -327,7 +327,7 @@ def test_sort_in_gemm1_matches_sort_launch(T, offset, skew, monkeypatch):
     """GEMM1 finding its row tiles from the top-k ids (and writing the sort's
     tables itself) gives bit-identical output and tables to the separate sort
     launch, for both GEMM1 variants that can do it (single-wave workgroups at
-    T <= 4, K split above): ragged T, other shard offsets, four row tiles per
+    T = 1, K split above): ragged T, other shard offsets, four row tiles per
     expert (skew) and no local token at all (offset 256)."""
     from flashinfer_amd import _lib, kernel
     log(f"test_sort_in_gemm1_matches_sort_launch[T={T}-off={offset}-skew={skew}]")
@@ -362,7 +362,7 @@ def test_route_in_gemm1_matches_separate_launches(T, offset, skew, force, monkey
     """GEMM1 routing every token itself (each workgroup, into LDS), sorting,
     and writing the top-k and the sort tables gives bit-identical output,
     top-k and tables to the routing and sort kernels: both GEMM1 shapes
-    (single-wave workgroups at T <= 4, K split above), T up to 64 when forced
+    (single-wave workgroups at T = 1, K split above), T up to 64 when forced
     on, other shard offsets, skewed routing and no local token."""
     from flashinfer_amd import _lib, kernel
     log(f"test_route_in_gemm1_matches_separate_launches[T={T}-off={offset}-skew={skew}]")
