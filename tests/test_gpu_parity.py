@@ -389,6 +389,27 @@ def test_route_in_gemm1_matches_separate_launches(T, offset, skew, force, monkey
         assert torch.equal(got[k], want[k]), k
 
 
+@pytest.mark.parametrize("T,fuse", [(1, ""), (4, ""), (64, ""), (300, ""), (1500, ""), (4, "1"),
+                                    (100, "1")])
+def test_fp32_bias_matches_bf16_bias(T, fuse, monkeypatch):
+    """routing_bias as fp32 holding the bf16 bias's values (exact) gives the
+    bf16 call's output bit for bit, through each front end: routing in GEMM1
+    (T=1), the sort in GEMM1 (T=4, 64), routing and sort kernels (T=300),
+    the chunked sort (T=1500) and the fused routing + sort kernel."""
+    from flashinfer_amd import kernel
+    log(f"test_fp32_bias_matches_bf16_bias[T={T}-fuse={fuse or 'default'}]")
+    if fuse:
+        monkeypatch.setenv("MI_MOE_FUSE_FRONT", fuse)
+    wl = W.make_workload("fp32_bias", T, 600 + T, local_expert_offset=32 * (T % 3))
+    ref = run_gpu(wl, fill=float("nan")).clone()
+    args = gpu_args(wl)
+    args[1] = args[1].float()
+    out = torch.full_like(ref, float("nan"))
+    kernel.run(*args, out)
+    torch.cuda.synchronize()
+    assert torch.equal(out.view(torch.int16), ref.view(torch.int16))
+
+
 def _check_sort_tables(ids, w, offset, got):
     """The sort entry point's tables against the oracle's local assignment."""
     from oracle import ref_moe as R
