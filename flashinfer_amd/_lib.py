@@ -29,7 +29,7 @@ MI_MOE_DTYPE_BF16 = 0
 MI_MOE_DTYPE_F32 = 1
 
 EXPORTED = ("mi_moe_workspace_size", "mi_moe_workspace_layout", "mi_moe_run",
-            "mi_moe_run_profiled", "mi_moe_route", "mi_moe_sort", "mi_moe_quantize_fp8",
+            "mi_moe_run_profiled", "mi_moe_run_bf16", "mi_moe_route", "mi_moe_sort", "mi_moe_quantize_fp8",
             "mi_moe_shape", "mi_moe_last_error", "mi_moe_version")
 NUM_PHASES = 5
 PHASES = ("route", "sort", "gemm1_swiglu", "gemm2", "combine")
@@ -79,6 +79,8 @@ def _bind(L: ctypes.CDLL) -> None:
     L.mi_moe_workspace_layout.restype = ctypes.c_int
     L.mi_moe_run.argtypes = [ctypes.POINTER(MiMoeArgs), ctypes.c_void_p]
     L.mi_moe_run.restype = ctypes.c_int
+    L.mi_moe_run_bf16.argtypes = [ctypes.POINTER(MiMoeArgs), ctypes.c_void_p, ctypes.c_void_p]
+    L.mi_moe_run_bf16.restype = ctypes.c_int
     L.mi_moe_run_profiled.argtypes = [ctypes.POINTER(MiMoeArgs), ctypes.c_void_p,
                                       ctypes.POINTER(ctypes.c_void_p), ctypes.c_int32]
     L.mi_moe_run_profiled.restype = ctypes.c_int

@@ -255,7 +255,10 @@ int mi_moe_quantize_fp8(const void* hidden_bf16, int64_t num_tokens, uint8_t* hi
     return MI_MOE_OK;
 }
 
-static int run_impl(const mi_moe_args* a, hipStream_t s, hipEvent_t const* ev) {
+// hidden_bf16 != nullptr: quantise it into a->hidden_states / scale first
+// (mi_moe_run_bf16), in the same launch as routing.
+static int run_impl(const mi_moe_args* a, hipStream_t s, hipEvent_t const* ev,
+                    const void* hidden_bf16 = nullptr) {
     g_last_error.clear();
     if (!a) return fail(MI_MOE_ERR_INVALID, "mi_moe_run: args is NULL");
     const int64_t T = a->num_tokens;
@@ -287,6 +290,8 @@ static int run_impl(const mi_moe_args* a, hipStream_t s, hipEvent_t const* ev) {
                            "gemm2_weights", "gemm2_weights_scale", "output", "workspace"};
     const size_t align[] = {16, (size_t)(a->bias_dtype == MI_MOE_DTYPE_F32 ? 16 : 8), 16, 4, 16,
                             4, 16, 4, 8, 256};
+    if (hidden_bf16 && !aligned(hidden_bf16, 16))
+        return fail(MI_MOE_ERR_INVALID, "mi_moe_run_bf16: hidden_bf16 is not 16-byte aligned");
     for (int i = 0; i < 10; ++i) {
         if (!ptrs[i]) return fail(MI_MOE_ERR_INVALID, "mi_moe_run: %s is NULL", names[i]);
         if (!aligned(ptrs[i], align[i]))
@@ -306,11 +311,20 @@ static int run_impl(const mi_moe_args* a, hipStream_t s, hipEvent_t const* ev) {
         if (ev && err == hipSuccess) err = hipEventRecord(ev[i], s);
     };
     const int bias_f32 = a->bias_dtype == MI_MOE_DTYPE_F32;
-    const Front front = pick_front(T, var.g1);
+    Front front = pick_front(T, var.g1);
+    if (hidden_bf16)  // routing runs with the quantiser; GEMM1 needs its output
+        front = (gemm1_sorts_supported((int)T, var.g1) && env_flag("MI_MOE_SORT_IN_GEMM1") != 0)
+                    ? Front::SORT_IN_GEMM1
+                    : Front::KERNELS;
     const FrontArgs fa{a->routing_logits, a->routing_bias, bias_f32, gemm1_bm(var.g1),
                        gemm2_bm(var.g2)};
     mark(0);
-    if (front == Front::FUSED) {
+    if (hidden_bf16) {
+        if (err == hipSuccess)
+            err = launch_quant_route(hidden_bf16, (int)T, (uint8_t*)a->hidden_states,
+                                     (float*)a->hidden_states_scale, a->routing_logits,
+                                     a->routing_bias, bias_f32, p.rsf, p.topk_ids, p.topk_w, s);
+    } else if (front == Front::FUSED) {
         if (err == hipSuccess)
             err = launch_route_sort(p, a->routing_logits, a->routing_bias, bias_f32, fa.bm1, fa.bm2,
                                     s);
@@ -352,6 +366,14 @@ static int run_impl(const mi_moe_args* a, hipStream_t s, hipEvent_t const* ev) {
 
 int mi_moe_run(const mi_moe_args* a, void* stream) {
     return run_impl(a, (hipStream_t)stream, nullptr);
+}
+
+int mi_moe_run_bf16(const mi_moe_args* a, const void* hidden_bf16, void* stream) {
+    if (!hidden_bf16) {
+        g_last_error.clear();
+        return fail(MI_MOE_ERR_INVALID, "mi_moe_run_bf16: hidden_bf16 is NULL");
+    }
+    return run_impl(a, (hipStream_t)stream, nullptr, hidden_bf16);
 }
 
 int mi_moe_run_profiled(const mi_moe_args* a, void* stream, void* const* events, int32_t n_events) {

@@ -170,6 +170,10 @@ hipError_t launch_gemm2(const Plan& p, const uint8_t* w2, const float* w2s, int 
                         hipStream_t s);
 hipError_t launch_combine(const Plan& p, uint16_t* out, hipStream_t s);
 hipError_t launch_quant_fp8(const void* x, int T, uint8_t* q, float* scale, hipStream_t s);
+// The quantiser and the routing kernel's work in one launch.
+hipError_t launch_quant_route(const void* x, int T, uint8_t* q, float* scale, const float* logits,
+                              const void* bias, int bias_is_f32, float rsf, int* topk_ids,
+                              float* topk_w, hipStream_t s);
 bool gemm2_combine_supported(int T);
 hipError_t launch_gemm2_combine(const Plan& p, const uint8_t* w2, const float* w2s, uint16_t* out,
                                 hipStream_t s);

@@ -13,7 +13,11 @@
 // NB blocks per token (all loads issued before any reduction), so the 16
 // scales it writes per block are one contiguous 64-byte run of
 // hidden_states_scale[b, t0 .. t0+15].
-#include "common.hpp"
+//
+// quant_route_kernel runs the same quantiser and the routing kernel's work
+// in one launch (they share no data): grid rows 0..HB/QUANT_NB-1 quantise a
+// 16-token group as above, and 4 more rows route its 16 tokens, one per wave.
+#include "route_impl.hpp"
 
 namespace mimoe {
 
@@ -25,9 +29,10 @@ __device__ __forceinline__ float bf16_hi(uint32_t w) { return __uint_as_float(w 
 
 constexpr int QUANT_NB = 2;  // blocks per token per workgroup (56 / 2 = 28 in y)
 
-__global__ __launch_bounds__(256) void quant_fp8_kernel(const uint16_t* __restrict__ x, int T,
-                                                         uint8_t* __restrict__ q,
-                                                         float* __restrict__ scale) {
+// Blocks by, by + HB/QUANT_NB, ... of the workgroup's 16 tokens.
+__device__ __forceinline__ void quant_group(const uint16_t* __restrict__ x, int T,
+                                            uint8_t* __restrict__ q, float* __restrict__ scale,
+                                            int by) {
     const int t = blockIdx.x * 16 + (threadIdx.x >> 4);  // token of this 16-lane row
     const int sub = threadIdx.x & 15;                    // 8-element slice of the block
     const bool live = t < T;                             // uniform across the row
@@ -37,7 +42,7 @@ __global__ __launch_bounds__(256) void quant_fp8_kernel(const uint16_t* __restri
     for (int j = 0; j < QUANT_NB; ++j) {
         amax[j] = 0.f;
         if (live) {
-            const int b = blockIdx.y + j * (HB / QUANT_NB);
+            const int b = by + j * (HB / QUANT_NB);
             const uint4 w = *reinterpret_cast<const uint4*>(x + (size_t)t * H + b * BLK + sub * 8);
             v[j][0] = bf16_lo(w.x); v[j][1] = bf16_hi(w.x);
             v[j][2] = bf16_lo(w.y); v[j][3] = bf16_hi(w.y);
@@ -57,7 +62,7 @@ __global__ __launch_bounds__(256) void quant_fp8_kernel(const uint16_t* __restri
     if (!live) return;
 #pragma unroll
     for (int j = 0; j < QUANT_NB; ++j) {
-        const int b = blockIdx.y + j * (HB / QUANT_NB);
+        const int b = by + j * (HB / QUANT_NB);
         const float s = fmaxf(amax[j], QUANT_EPS) / FP8_MAX;
 #pragma unroll
         for (int i = 0; i < 8; ++i) v[j][i] = fminf(fmaxf(v[j][i] / s, -FP8_MAX), FP8_MAX);
@@ -71,11 +76,52 @@ __global__ __launch_bounds__(256) void quant_fp8_kernel(const uint16_t* __restri
     }
 }
 
+__global__ __launch_bounds__(256) void quant_fp8_kernel(const uint16_t* __restrict__ x, int T,
+                                                         uint8_t* __restrict__ q,
+                                                         float* __restrict__ scale) {
+    quant_group(x, T, q, scale, blockIdx.y);
+}
+
+__global__ __launch_bounds__(256) void quant_route_kernel(
+    const uint16_t* __restrict__ x, int T, uint8_t* __restrict__ q, float* __restrict__ scale,
+    const float* __restrict__ logits, const void* __restrict__ bias, int bias_is_f32, float rsf,
+    int* __restrict__ topk_ids, float* __restrict__ topk_w) {
+    constexpr int QROWS = HB / QUANT_NB;
+    if ((int)blockIdx.y < QROWS) {
+        quant_group(x, T, q, scale, blockIdx.y);
+        return;
+    }
+    const int lane = threadIdx.x & 63;
+    const int t = blockIdx.x * 16 + (blockIdx.y - QROWS) * 4 + (threadIdx.x >> 6);
+    if (t >= T) return;
+    int ids[TOPK];
+    float w[TOPK];
+    route_token(logits + (size_t)t * EG, bias, bias_is_f32, rsf, lane, ids, w);
+    if (lane == 0) {
+        int4* io = reinterpret_cast<int4*>(topk_ids + (size_t)t * TOPK);
+        float4* wo = reinterpret_cast<float4*>(topk_w + (size_t)t * TOPK);
+        io[0] = make_int4(ids[0], ids[1], ids[2], ids[3]);
+        io[1] = make_int4(ids[4], ids[5], ids[6], ids[7]);
+        wo[0] = make_float4(w[0], w[1], w[2], w[3]);
+        wo[1] = make_float4(w[4], w[5], w[6], w[7]);
+    }
+}
+
 hipError_t launch_quant_fp8(const void* x, int T, uint8_t* q, float* scale, hipStream_t s) {
     if (T <= 0) return hipSuccess;
     static_assert(HB % QUANT_NB == 0, "blocks per workgroup");
     hipLaunchKernelGGL(quant_fp8_kernel, dim3((T + 15) / 16, HB / QUANT_NB), dim3(256), 0, s,
                        (const uint16_t*)x, T, q, scale);
+    return hipGetLastError();
+}
+
+hipError_t launch_quant_route(const void* x, int T, uint8_t* q, float* scale, const float* logits,
+                              const void* bias, int bias_is_f32, float rsf, int* topk_ids,
+                              float* topk_w, hipStream_t s) {
+    if (T <= 0) return hipSuccess;
+    hipLaunchKernelGGL(quant_route_kernel, dim3((T + 15) / 16, HB / QUANT_NB + 4), dim3(256), 0, s,
+                       (const uint16_t*)x, T, q, scale, logits, bias, bias_is_f32, rsf, topk_ids,
+                       topk_w);
     return hipGetLastError();
 }
 

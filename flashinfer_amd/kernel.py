@@ -158,9 +158,40 @@ def run_profiled(*args, events):
     _call(*args, events)
 
 
+@torch.no_grad()
+def run_bf16(routing_logits: torch.Tensor, routing_bias: torch.Tensor, hidden: torch.Tensor,
+             gemm1_weights: torch.Tensor, gemm1_weights_scale: torch.Tensor,
+             gemm2_weights: torch.Tensor, gemm2_weights_scale: torch.Tensor,
+             local_expert_offset: int, routed_scaling_factor: float, output: torch.Tensor,
+             hidden_states: torch.Tensor | None = None,
+             hidden_states_scale: torch.Tensor | None = None):
+    """``run`` from bf16 activations ``hidden`` [T, H]: the FP8 quantiser of
+    ``quantize_activations`` and routing share the call's first launch, then
+    the layer runs as in ``run`` (``mi_moe_run_bf16``). Returns the
+    ``(hidden_states, hidden_states_scale)`` pair it wrote (passed in, or
+    allocated); the output equals ``quantize_activations`` followed by
+    ``run`` bit for bit. No counterpart in the reference, whose inputs arrive
+    quantised."""
+    if not isinstance(hidden, torch.Tensor) or hidden.dim() != 2:
+        raise ValueError("hidden must be a 2-D tensor [T, H]")
+    T, H = int(hidden.shape[0]), int(hidden.shape[1])
+    dev = hidden.device
+    if hidden_states is None:
+        hidden_states = torch.empty(T, H, dtype=FP8, device=dev)
+    if hidden_states_scale is None:
+        hidden_states_scale = torch.empty(H // BLOCK, T, dtype=torch.float32, device=dev)
+    for t, n in ((hidden_states, "hidden_states"), (hidden_states_scale, "hidden_states_scale")):
+        if isinstance(t, torch.Tensor) and not t.is_contiguous():
+            raise ValueError(f"{n} must be contiguous (it is written in place)")
+    _call(routing_logits, routing_bias, hidden_states, hidden_states_scale, gemm1_weights,
+          gemm1_weights_scale, gemm2_weights, gemm2_weights_scale, local_expert_offset,
+          routed_scaling_factor, output, None, hidden_bf16=hidden)
+    return hidden_states, hidden_states_scale
+
+
 def _call(routing_logits, routing_bias, hidden_states, hidden_states_scale, gemm1_weights,
           gemm1_weights_scale, gemm2_weights, gemm2_weights_scale, local_expert_offset,
-          routed_scaling_factor, output, events):
+          routed_scaling_factor, output, events, hidden_bf16=None):
     if not isinstance(routing_logits, torch.Tensor) or routing_logits.dim() != 2:
         raise ValueError("routing_logits must be a 2-D tensor [T, 256]")
     T = int(routing_logits.shape[0])
@@ -179,6 +210,9 @@ def _call(routing_logits, routing_bias, hidden_states, hidden_states_scale, gemm
     _expect(output, "output", (torch.bfloat16,), (T, H))
     tensors = (routing_logits, routing_bias, hidden_states, hidden_states_scale, gemm1_weights,
                gemm1_weights_scale, gemm2_weights, gemm2_weights_scale, output)
+    if hidden_bf16 is not None:
+        _expect(hidden_bf16, "hidden", (torch.bfloat16,), (T, H))
+        tensors = tensors + (hidden_bf16,)
     device = output.device
     if device.type != "cuda":
         raise ValueError("run() needs tensors on a ROCm GPU (device type 'cuda'); there is no "
@@ -191,7 +225,7 @@ def _call(routing_logits, routing_bias, hidden_states, hidden_states_scale, gemm
     if T == 0 and events is None:
         return
 
-    ins = [t.contiguous() for t in tensors[:-1]]
+    ins = [t.contiguous() for t in tensors[:8]]
     out = output if output.is_contiguous() else torch.empty_like(
         output, memory_format=torch.contiguous_format)
     with torch.cuda.device(device):
@@ -210,7 +244,11 @@ def _call(routing_logits, routing_bias, hidden_states, hidden_states_scale, gemm
             bias_dtype=(_lib.MI_MOE_DTYPE_BF16 if ins[1].dtype == torch.bfloat16
                         else _lib.MI_MOE_DTYPE_F32),
             reserved=0, workspace=ws.data_ptr(), workspace_bytes=ws.numel())
-        if events is None:
+        if hidden_bf16 is not None:
+            x = hidden_bf16.contiguous()
+            _lib.check(L.mi_moe_run_bf16(ctypes.byref(args), ctypes.c_void_p(x.data_ptr()),
+                                         ctypes.c_void_p(stream)), L)
+        elif events is None:
             _lib.check(L.mi_moe_run(ctypes.byref(args), ctypes.c_void_p(stream)), L)
         else:
             handles = []

@@ -99,6 +99,15 @@ int mi_moe_run(const mi_moe_args* args, void* stream);
 int mi_moe_run_profiled(const mi_moe_args* args, void* stream, void* const* events,
                         int32_t n_events);
 
+/* mi_moe_run from bf16 activations: quantises hidden_bf16 (bf16 [T, 7168],
+ * 16-byte aligned) into args->hidden_states and args->hidden_states_scale,
+ * which are written (same formula and layout as mi_moe_quantize_fp8), and
+ * routes the tokens in that same first launch; then the call continues as
+ * mi_moe_run. No counterpart in the reference, whose inputs arrive quantised:
+ * it equals mi_moe_quantize_fp8 followed by mi_moe_run, one launch shorter,
+ * for callers that start from bf16 hidden states. */
+int mi_moe_run_bf16(const mi_moe_args* args, const void* hidden_bf16, void* stream);
+
 /* Routing only (kernel.py:371-457 without the local filter): writes global
  * top-8 ids (int32 [T, 8], selection order) and weights (fp32 [T, 8]). */
 int mi_moe_route(const float* routing_logits, const void* routing_bias, int32_t bias_dtype,

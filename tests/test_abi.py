@@ -112,6 +112,19 @@ def test_route_rejects_before_launch():
     assert L.mi_moe_route(None, None, 0, 0, 2.5, None, None, None) == _lib.MI_MOE_OK
 
 
+def test_run_bf16_rejects_before_launch():
+    L = _lib.lib()
+    a = _args()
+    assert L.mi_moe_run_bf16(ctypes.byref(a), None, None) == _lib.MI_MOE_ERR_INVALID
+    assert b"hidden_bf16" in L.mi_moe_last_error()
+    assert L.mi_moe_run_bf16(ctypes.byref(a), ctypes.c_void_p((1 << 30) + 8), None) \
+        == _lib.MI_MOE_ERR_INVALID
+    assert b"aligned" in L.mi_moe_last_error()
+    # the checks of mi_moe_run apply as well (workspace_bytes is 0 here)
+    assert L.mi_moe_run_bf16(ctypes.byref(a), ctypes.c_void_p(1 << 30), None) \
+        == _lib.MI_MOE_ERR_WORKSPACE
+
+
 def test_sort_rejects_before_launch():
     L = _lib.lib()
     fake = 1 << 20  # never dereferenced: every check runs before a launch

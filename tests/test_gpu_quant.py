@@ -103,3 +103,29 @@ def test_quantize_rejects_bad_arguments():
         kernel.quantize_activations(torch.zeros(2, 100, dtype=torch.bfloat16, device="cuda"))
     q, s = kernel.quantize_activations(torch.zeros(0, H, dtype=torch.bfloat16, device="cuda"))
     assert q.shape == (0, H) and s.shape == (H // 128, 0)
+
+
+@pytest.mark.parametrize("T", [1, 4, 16, 64, 300, 1500])
+def test_run_bf16_matches_quantize_then_run(T):
+    """run_bf16 (quantiser and routing in one launch, then the layer) writes
+    the fp8 pair of quantize_activations and the output of run on it, bit for
+    bit, through each front end (T=1..64 sort in GEMM1, 300 sort kernel,
+    1500 chunked sort)."""
+    from flashinfer_amd import kernel
+    from _helpers import gpu_args
+    log(f"test_run_bf16_matches_quantize_then_run[T={T}]")
+    wl = W.make_workload("run_bf16", T, 700 + T, local_expert_offset=32 * (T % 3))
+    g = torch.Generator().manual_seed(T)
+    x = (torch.randn(T, H, generator=g) * 0.5).to(torch.bfloat16).cuda()
+    args = gpu_args(wl)
+    q, s = kernel.quantize_activations(x)
+    args[2], args[3] = q, s
+    ref = torch.full((T, H), float("nan"), dtype=torch.bfloat16, device="cuda")
+    kernel.run(*args, ref)
+    out = torch.full_like(ref, float("nan"))
+    rest = args[:2] + args[4:]
+    q2, s2 = kernel.run_bf16(rest[0], rest[1], x, *rest[2:], out)
+    torch.cuda.synchronize()
+    assert torch.equal(q2.view(torch.uint8), q.view(torch.uint8))
+    assert torch.equal(s2, s)
+    assert torch.equal(out.view(torch.int16), ref.view(torch.int16))
