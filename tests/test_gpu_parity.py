@@ -185,7 +185,7 @@ def test_skew_all_rows_on_biased_experts():
     assert torch.equal(eoff, want)
 
 
-def _random_configs(n=20, seed=2026):
+def _random_workloads(n=20, seed=2026):
     """Seeded (T, offset, skew, routed_scaling_factor) draws: ragged T from 1
     to ~1100 (weighted to decode sizes), shard offsets that are negative,
     unaligned or near the end of the 256 experts."""
@@ -201,11 +201,11 @@ def _random_configs(n=20, seed=2026):
     return out
 
 
-@pytest.mark.parametrize("i,T,offset,skew,rsf", _random_configs())
-def test_random_configs(i, T, offset, skew, rsf):
+@pytest.mark.parametrize("i,T,offset,skew,rsf", _random_workloads())
+def test_random_workloads(i, T, offset, skew, rsf):
     """Output against the oracle on seeded random shapes and shard offsets
     through the default kernel choice for each T."""
-    log(f"test_random_configs[{i}: T={T} off={offset} skew={skew} rsf={rsf}]")
+    log(f"test_random_workloads[{i}: T={T} off={offset} skew={skew} rsf={rsf}]")
     wl = W.make_workload(f"random_{i}", T, 5000 + i, local_expert_offset=offset, skew=skew,
                          routed_scaling_factor=rsf)
     _route_check(wl)
