@@ -58,8 +58,24 @@ def _expect(t: torch.Tensor, name: str, dtypes, shape) -> None:
         raise TypeError(f"{name} must be a torch.Tensor, got {type(t).__name__}")
     if t.dtype not in dtypes:
         raise TypeError(f"{name} must have dtype in {[str(d) for d in dtypes]}, got {t.dtype}")
-    if tuple(t.shape) != tuple(shape):
+    if t.shape != shape:
         raise ValueError(f"{name} must have shape {tuple(shape)}, got {tuple(t.shape)}")
+
+
+# The per-call host path matters at small T, where the GPU work of a call is
+# ~11 us: the raw HIP stream handle of the current stream, without building a
+# torch Stream object (torch's own accessor; None if this torch lacks it), and
+# workspace sizes cached per (T, shape).
+_RAW_STREAM = getattr(torch._C, "_cuda_getCurrentRawStream", None)
+_WS_SIZES: dict = {}
+
+
+def _ws_size(T: int, shape) -> int:
+    key = (T, shape)
+    n = _WS_SIZES.get(key)
+    if n is None:
+        n = _WS_SIZES[key] = _lib.workspace_size(T, shape)
+    return n
 
 
 def _scalar(x, kind):
@@ -124,7 +140,6 @@ def _emit_phase_timing(args, T: int) -> None:
         pass
 
 
-@torch.no_grad()
 def run(
     routing_logits: torch.Tensor,
     routing_bias: torch.Tensor,
@@ -158,7 +173,6 @@ def run_profiled(*args, events):
     _call(*args, events)
 
 
-@torch.no_grad()
 def run_bf16(routing_logits: torch.Tensor, routing_bias: torch.Tensor, hidden: torch.Tensor,
              gemm1_weights: torch.Tensor, gemm1_weights_scale: torch.Tensor,
              gemm2_weights: torch.Tensor, gemm2_weights_scale: torch.Tensor,
@@ -228,39 +242,51 @@ def _call(routing_logits, routing_bias, hidden_states, hidden_states_scale, gemm
     ins = [t.contiguous() for t in tensors[:8]]
     out = output if output.is_contiguous() else torch.empty_like(
         output, memory_format=torch.contiguous_format)
-    with torch.cuda.device(device):
-        cur = torch.cuda.current_stream(device)
-        stream = cur.cuda_stream
-        L = _lib.lib(shape)
-        need = _lib.workspace_size(T, shape)
-        ws = _workspace(device, stream, need)
-        args = _lib.MiMoeArgs(
-            routing_logits=ins[0].data_ptr(), routing_bias=ins[1].data_ptr(),
-            hidden_states=ins[2].data_ptr(), hidden_states_scale=ins[3].data_ptr(),
-            gemm1_weights=ins[4].data_ptr(), gemm1_weights_scale=ins[5].data_ptr(),
-            gemm2_weights=ins[6].data_ptr(), gemm2_weights_scale=ins[7].data_ptr(),
-            local_expert_offset=offset, routed_scaling_factor=rsf,
-            output=out.data_ptr(), num_tokens=T,
-            bias_dtype=(_lib.MI_MOE_DTYPE_BF16 if ins[1].dtype == torch.bfloat16
-                        else _lib.MI_MOE_DTYPE_F32),
-            reserved=0, workspace=ws.data_ptr(), workspace_bytes=ws.numel())
-        if hidden_bf16 is not None:
-            x = hidden_bf16.contiguous()
-            _lib.check(L.mi_moe_run_bf16(ctypes.byref(args), ctypes.c_void_p(x.data_ptr()),
-                                         ctypes.c_void_p(stream)), L)
-        elif events is None:
-            _lib.check(L.mi_moe_run(ctypes.byref(args), ctypes.c_void_p(stream)), L)
-        else:
-            handles = []
-            for ev in events:
-                if ev.cuda_event == 0:  # torch creates the HIP event on first record
-                    ev.record(cur)
-                handles.append(ev.cuda_event)
-            arr = (ctypes.c_void_p * len(handles))(*handles)
-            _lib.check(L.mi_moe_run_profiled(ctypes.byref(args), ctypes.c_void_p(stream),
-                                             arr, len(handles)), L)
+    if (events is None and _RAW_STREAM is not None
+            and device.index == torch.cuda.current_device()):
+        # hot path: no device switch and no torch Stream object
+        _issue(shape, T, device, _RAW_STREAM(device.index), None, ins, out, offset, rsf, None,
+               hidden_bf16)
+    else:
+        with torch.cuda.device(device):
+            cur = torch.cuda.current_stream(device)
+            _issue(shape, T, device, cur.cuda_stream, cur, ins, out, offset, rsf, events,
+                   hidden_bf16)
     if out is not output:
-        output.copy_(out)
+        with torch.no_grad():  # output may be a leaf that requires grad
+            output.copy_(out)
+
+
+def _issue(shape, T, device, stream, cur, ins, out, offset, rsf, events, hidden_bf16):
+    """Fills the argument block and calls the library on `stream`."""
+    L = _lib.lib(shape)
+    need = _ws_size(T, shape)
+    ws = _workspace(device, stream, need)
+    args = _lib.MiMoeArgs(
+        routing_logits=ins[0].data_ptr(), routing_bias=ins[1].data_ptr(),
+        hidden_states=ins[2].data_ptr(), hidden_states_scale=ins[3].data_ptr(),
+        gemm1_weights=ins[4].data_ptr(), gemm1_weights_scale=ins[5].data_ptr(),
+        gemm2_weights=ins[6].data_ptr(), gemm2_weights_scale=ins[7].data_ptr(),
+        local_expert_offset=offset, routed_scaling_factor=rsf,
+        output=out.data_ptr(), num_tokens=T,
+        bias_dtype=(_lib.MI_MOE_DTYPE_BF16 if ins[1].dtype == torch.bfloat16
+                    else _lib.MI_MOE_DTYPE_F32),
+        reserved=0, workspace=ws.data_ptr(), workspace_bytes=ws.numel())
+    if hidden_bf16 is not None:
+        x = hidden_bf16.contiguous()
+        _lib.check(L.mi_moe_run_bf16(ctypes.byref(args), ctypes.c_void_p(x.data_ptr()),
+                                     ctypes.c_void_p(stream)), L)
+    elif events is None:
+        _lib.check(L.mi_moe_run(ctypes.byref(args), ctypes.c_void_p(stream)), L)
+    else:
+        handles = []
+        for ev in events:
+            if ev.cuda_event == 0:  # torch creates the HIP event on first record
+                ev.record(cur)
+            handles.append(ev.cuda_event)
+        arr = (ctypes.c_void_p * len(handles))(*handles)
+        _lib.check(L.mi_moe_run_profiled(ctypes.byref(args), ctypes.c_void_p(stream),
+                                         arr, len(handles)), L)
 
 
 def route(routing_logits: torch.Tensor, routing_bias: torch.Tensor, routed_scaling_factor: float):
