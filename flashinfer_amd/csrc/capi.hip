@@ -134,9 +134,10 @@ Variants pick_variants(int64_t T) {
     // waves) while an expert has at most a few row tiles, 64-column GEMM2 waves from T = 64, the
     // wide kernels (register-ring weights, LDS activations) for roughly 5 to
     // 70 rows per expert (GEMM2 from ~10 to ~15), the LDS-tiled kernels beyond.
-    // GEMM2 with the combine in one launch fewer where launches dominate
-    if (T <= 1) v = {5, VARIANT_GEMM2_COMBINE};
-    else if (T <= 4) v = {16, VARIANT_GEMM2_COMBINE};
+    // GEMM2 with the combine (K split over its 4 waves, which keeps them all
+    // busy with fewer than 4 row tiles): one launch fewer where launches dominate
+    if (T <= 1) v = {5, VARIANT_GEMM2_COMBINE_KS};
+    else if (T <= 4) v = {16, VARIANT_GEMM2_COMBINE_KS};
     else if (T <= 32) v = {16, 5};
     else if (T <= 128) v = {16, 14};
     else if (T <= 192) v = {15, 13};
@@ -347,14 +348,20 @@ static int run_impl(const mi_moe_args* a, hipStream_t s, hipEvent_t const* ev,
                                a->gemm1_weights_scale, var.g1, s);
     }
     mark(3);
-    const bool fused = var.g2 == VARIANT_GEMM2_COMBINE && gemm2_combine_supported(p.T);
+    const bool fused_ks = var.g2 == VARIANT_GEMM2_COMBINE_KS && gemm2_combine_supported(p.T);
+    const bool fused =
+        fused_ks || (var.g2 == VARIANT_GEMM2_COMBINE && gemm2_combine_supported(p.T));
     if (err == hipSuccess) {
-        if (fused)
+        if (fused_ks)
+            err = launch_gemm2_combine_ks(p, a->gemm2_weights, a->gemm2_weights_scale,
+                                          (uint16_t*)a->output, s);
+        else if (fused)
             err = launch_gemm2_combine(p, a->gemm2_weights, a->gemm2_weights_scale,
                                        (uint16_t*)a->output, s);
         else
             err = launch_gemm2(p, a->gemm2_weights, a->gemm2_weights_scale,
-                               var.g2 == VARIANT_GEMM2_COMBINE ? 0 : var.g2, s);
+                               (var.g2 == VARIANT_GEMM2_COMBINE ||
+                                var.g2 == VARIANT_GEMM2_COMBINE_KS) ? 0 : var.g2, s);
     }
     mark(4);
     if (err == hipSuccess && !fused) err = launch_combine(p, (uint16_t*)a->output, s);

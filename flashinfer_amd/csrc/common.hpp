@@ -175,6 +175,10 @@ hipError_t launch_quant_route(const void* x, int T, uint8_t* q, float* scale, co
                               const void* bias, int bias_is_f32, float rsf, int* topk_ids,
                               float* topk_w, hipStream_t s);
 bool gemm2_combine_supported(int T);
+// The same with the 16 k-blocks split over the 4 waves (every wave runs every
+// row tile): more waves in flight when there are fewer than 4 row tiles.
+hipError_t launch_gemm2_combine_ks(const Plan& p, const uint8_t* w2, const float* w2s,
+                                   uint16_t* out, hipStream_t s);
 hipError_t launch_gemm2_combine(const Plan& p, const uint8_t* w2, const float* w2s, uint16_t* out,
                                 hipStream_t s);
 hipError_t launch_gemm1_tile(const Plan& p, const uint8_t* hs, const float* hs_scale,
@@ -192,11 +196,15 @@ hipError_t launch_gemm2_wide(const Plan& p, const uint8_t* w2, const float* w2s,
 // (see the launchers), 10 GEMM2 fused with the combine, 15 "wide" tiles
 // (64 rows for GEMM1, 32 for GEMM2; weights through a per-wave register
 // ring, activations through LDS) for medium row counts, 16 GEMM1 streaming
-// with K split over 4 waves of a workgroup. An id without a kernel of its own
-// in one GEMM (9 and 16 for GEMM2) runs that GEMM's default stream shape.
-constexpr int NUM_VARIANTS = 17;
-// GEMM2 variant that also performs the combine (decode sizes only).
+// with K split over 4 waves of a workgroup, 17 GEMM2 fused with the combine
+// with K split over its 4 waves. An id without a kernel of its own in one GEMM
+// (9, 10 and 17 for GEMM1, 9 and 16 for GEMM2) runs that GEMM's default
+// stream shape.
+constexpr int NUM_VARIANTS = 18;
+// GEMM2 variants that also perform the combine (decode sizes only): tiles
+// dealt to the 4 waves, or k-blocks split over them.
 constexpr int VARIANT_GEMM2_COMBINE = 10;
+constexpr int VARIANT_GEMM2_COMBINE_KS = 17;
 
 // Row-tile height of each GEMM variant (rows of one expert per workgroup).
 int gemm1_bm(int variant);

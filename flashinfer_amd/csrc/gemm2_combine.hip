@@ -36,12 +36,16 @@ __device__ __forceinline__ UnitInfo unit_info(const int* meta, int u) {
     return r;
 }
 
-template <int D>
+template <int D, int KS = 1>
 __global__ __launch_bounds__(256) void gemm2_combine_kernel(Plan p, const uint8_t* __restrict__ w2,
                                                             const float* __restrict__ w2s,
                                                             uint16_t* __restrict__ out) {
-    static_assert(IB % D == 0, "ring depth must divide the k-blocks of a tile");
-    static_assert(D < IB && IB <= 64, "the load side stays in the tile; one lane per k-block scale");
+    // KS == 1: tile u goes to wave u % 4, which runs all IB k-blocks of it.
+    // KS == 4: every wave runs every tile, over k-blocks [wave*KBW, +KBW).
+    static_assert(KS == 1 || KS == 4, "k split over the 4 waves or none");
+    constexpr int KBW = IB / KS;  // k-blocks of a tile per wave
+    static_assert(IB % KS == 0 && KBW % D == 0, "ring depth must divide a wave's k-blocks of a tile");
+    static_assert(D < KBW && IB <= 64, "the load side stays in the tile; one lane per k-block scale");
     extern __shared__ float acc_lds[];  // [4 waves][T][16]
     const int T = p.T;
     const int tid = threadIdx.x;
@@ -55,8 +59,11 @@ __global__ __launch_bounds__(256) void gemm2_combine_kernel(Plan p, const uint8_
     __syncthreads();
 
     const int total = p.meta[META_MTILE2 + EL];
-    const int nunits = wave < total ? (total - wave + 3) / 4 : 0;
-    const int nsteps = nunits * IB;
+    const int nunits = KS > 1 ? total : (wave < total ? (total - wave + 3) / 4 : 0);
+    const int nsteps = nunits * KBW;
+    const int ustep = KS > 1 ? 1 : 4;           // tile index step between a wave's tiles
+    const int u0 = KS > 1 ? 0 : wave;           // a wave's first tile
+    const int kb0 = KS > 1 ? wave * KBW : 0;    // a wave's first k-block of each tile
     float* my_acc = acc_lds + wave * T * 16;
 
     if (nsteps > 0) {
@@ -66,7 +73,7 @@ __global__ __launch_bounds__(256) void gemm2_combine_kernel(Plan p, const uint8_
         // before the compute side needs it): block scales of the 16 k-blocks,
         // and the token and routing weight of the lane's 4 output rows.
         // Lane q < IB holds the scale of k-block q; readlane picks it.
-        UnitInfo lu = unit_info(p.meta, wave);
+        UnitInfo lu = unit_info(p.meta, u0);
         float lu_sb = 0.f;
         int lu_tok[4];
         float lu_w[4];
@@ -88,8 +95,9 @@ __global__ __launch_bounds__(256) void gemm2_combine_kernel(Plan p, const uint8_
             }
         };
         auto load = [&](int d, int s) __attribute__((always_inline)) {
-            const int kb = s % IB;  // step s: k-block kb of the wave's tile s / IB
-            if (kb == 0 && s > 0) fetch_unit(wave + 4 * (s / IB));
+            // step s: k-block kb of the wave's (s / KBW)-th tile
+            const int kb = kb0 + s % KBW;
+            if (s % KBW == 0 && s > 0) fetch_unit(u0 + ustep * (s / KBW));
             const uint8_t* bp = w2 + ((size_t)lu.e * H + n0 + r) * I + g * 16 + kb * BLK;
             b[d] = ld_frag(bp);
             const uint16_t* ap =
@@ -100,9 +108,9 @@ __global__ __launch_bounds__(256) void gemm2_combine_kernel(Plan p, const uint8_
             a[d][3] = ld16(ap + 72);
         };
         auto compute = [&](int d, int s) __attribute__((always_inline)) {
-            const int kb = s % IB;
-            if (kb == 0) {
-                // The load side is D < IB steps ahead, so it is still in this tile.
+            const int kb = kb0 + s % KBW;
+            if (s % KBW == 0) {
+                // The load side is D < KBW steps ahead, so it is still in this tile.
                 cu = lu;
                 cu_sb = lu_sb;
 #pragma unroll
@@ -123,7 +131,7 @@ __global__ __launch_bounds__(256) void gemm2_combine_kernel(Plan p, const uint8_
             acc[1] += pr[1] * sb;
             acc[2] += pr[2] * sb;
             acc[3] += pr[3] * sb;
-            if (kb == IB - 1) {
+            if (s % KBW == KBW - 1) {
 #pragma unroll
                 for (int i = 0; i < 4; ++i) {
                     if (g * 4 + i < cu.nrows) my_acc[cu_tok[i] * 16 + r] += cu_w[i] * acc[i];
@@ -132,7 +140,7 @@ __global__ __launch_bounds__(256) void gemm2_combine_kernel(Plan p, const uint8_
             }
         };
 
-        fetch_unit(wave);
+        fetch_unit(u0);
 #pragma unroll
         for (int d = 0; d < D; ++d) load(d, d);
 #pragma unroll 1
@@ -166,6 +174,17 @@ hipError_t launch_gemm2_combine(const Plan& p, const uint8_t* w2, const float* w
     const size_t lds = (size_t)4 * p.T * 16 * sizeof(float);
     constexpr int D = IB % 4 == 0 ? 4 : 2;  // ring depth must divide the shape's k-blocks
     hipLaunchKernelGGL((gemm2_combine_kernel<D>), dim3(H / 16), dim3(256), lds, s, p, w2, w2s, out);
+    return hipGetLastError();
+}
+
+hipError_t launch_gemm2_combine_ks(const Plan& p, const uint8_t* w2, const float* w2s,
+                                   uint16_t* out, hipStream_t s) {
+    if (p.T <= 0) return hipSuccess;
+    const size_t lds = (size_t)4 * p.T * 16 * sizeof(float);
+    constexpr int KBW = IB / 4;
+    constexpr int D = (KBW % 2 == 0 && KBW > 2) ? 2 : 1;  // divides a wave's k-blocks, below them
+    hipLaunchKernelGGL((gemm2_combine_kernel<D, 4>), dim3(H / 16), dim3(256), lds, s, p, w2, w2s,
+                       out);
     return hipGetLastError();
 }
 
