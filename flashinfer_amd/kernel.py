@@ -17,6 +17,7 @@ from __future__ import annotations
 import ctypes
 import json
 import os
+import threading
 from pathlib import Path
 
 import torch
@@ -28,11 +29,22 @@ from . import _lib
 H, I, E_GLOBAL, E_LOCAL, BLOCK = 7168, 2048, 256, 32, 128
 FP8 = torch.float8_e4m3fn
 
-_workspaces: dict = {}
+# Workspaces cached per thread and (device, stream): calls on one stream from
+# two Python threads would otherwise share one, and their kernels can
+# interleave on the stream.
+_tls = threading.local()
+
+
+def _workspace_cache() -> dict:
+    c = getattr(_tls, "ws", None)
+    if c is None:
+        c = _tls.ws = {}
+    return c
 
 
 def _workspace(device: torch.device, stream: int, nbytes: int) -> torch.Tensor:
     key = (device.index, stream)
+    _workspaces = _workspace_cache()
     ws = _workspaces.get(key)
     if ws is None or ws.numel() < nbytes:
         # round up so a slowly growing T does not reallocate every call
@@ -390,7 +402,8 @@ def quantize_activations(hidden: torch.Tensor, hidden_states: torch.Tensor | Non
 
 
 def last_workspace(device: torch.device | None = None) -> torch.Tensor:
-    """The cached workspace of the current stream (for staged parity checks)."""
+    """The calling thread's cached workspace of the current stream (for staged
+    parity checks)."""
     device = device or torch.device("cuda", torch.cuda.current_device())
     stream = torch.cuda.current_stream(device).cuda_stream
-    return _workspaces[(device.index, stream)]
+    return _workspace_cache()[(device.index, stream)]

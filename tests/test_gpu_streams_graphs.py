@@ -85,3 +85,34 @@ def test_graph_capture_and_replay(name, other):
         log(f"  replay {i}: equal={torch.equal(_bits(got), _bits(eager))}")
         assert torch.isfinite(got.float()).all()
         assert torch.equal(_bits(got), _bits(eager))
+
+
+def test_two_threads_one_stream():
+    """Two Python threads calling run on the same stream at once each get
+    their own workspace, so interleaved kernels of the two calls cannot mix
+    tables: every output equals the single-threaded one bit for bit."""
+    import threading
+    log("test_two_threads_one_stream")
+    wls = [W.standard("c1_t16"), W.standard("c1_t64")]
+    refs = [run_gpu(wl).clone() for wl in wls]
+    errors = []
+
+    def worker(i):
+        try:
+            args = gpu_args(wls[i])
+            out = torch.empty_like(refs[i])
+            for _ in range(20):
+                kernel.run(*args, out)
+                torch.cuda.current_stream().synchronize()
+                if not torch.equal(out.view(torch.int16), refs[i].view(torch.int16)):
+                    errors.append(i)
+                    return
+        except Exception as exc:  # reported below
+            errors.append(repr(exc))
+
+    threads = [threading.Thread(target=worker, args=(i,)) for i in range(2)]
+    for t in threads:
+        t.start()
+    for t in threads:
+        t.join(timeout=120)
+    assert not errors, errors
