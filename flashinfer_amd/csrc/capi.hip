@@ -5,9 +5,9 @@
 // nothing and reports why through mi_moe_last_error(). The call enqueues
 // route -> sort -> GEMM1+SwiGLU -> GEMM2 -> combine on the caller's stream
 // with grids sized from T alone: no device-to-host copy, no host sync
-// (the reference syncs three times, kernel.py:572, :718, :773). At decode
-// sizes routing and the sort fold into GEMM1 (T = 1), or the sort alone does
-// (T <= 64); see pick_front.
+// (the reference syncs three times, kernel.py:572, :718, :773). Routing and
+// the sort fold into GEMM1 at T = 1, the sort alone up to T = 64 and from
+// T = 129 to 256 (the stream and wide GEMM1 kernels); see pick_front.
 #include <math.h>
 #include <stdarg.h>
 #include <stdio.h>
@@ -118,7 +118,8 @@ Front pick_front(int64_t T, int g1) {
     const bool g1_can = gemm1_sorts_supported((int)T, g1);
     const bool fused_ok = route_sort_supported((int)T);
     if (fuse == 1 && fused_ok) return Front::FUSED;
-    if (g1_can && (route == -1 ? T <= ROUTE_IN_GEMM1_MAX_T : route == 1)) return Front::ROUTE_IN_GEMM1;
+    if (gemm1_routes_supported((int)T, g1) && (route == -1 ? T <= ROUTE_IN_GEMM1_MAX_T : route == 1))
+        return Front::ROUTE_IN_GEMM1;
     // Routing as its own launch plus the sort inside the K-split GEMM1 beats
     // the fused routing + sort kernel from T = 2 when the shard has slots
     // (measured per call, four seeds at T = 3..4: 1.5-4 us; T = 5..8: 2-3 us;

@@ -158,11 +158,16 @@ struct FrontArgs {
     int bias_is_f32;
     int bm1, bm2;         // row-tile heights of the GEMM1 / GEMM2 kernels for the tables
 };
-// GEMM1 stream variants 16 and 5 with FRONT_SORT or FRONT_ROUTE (T <= 64):
-// they find their row tiles themselves and write the sort's tables (and, with
-// FRONT_ROUTE, the top-k) for the kernels after them, so no sort (or routing)
-// launch precedes them.
+// GEMM1 stream variants 16 and 5 with FRONT_SORT or FRONT_ROUTE (T <= 64),
+// and the wide variant 15 with FRONT_SORT (T <= 256): they find their row
+// tiles themselves and write the sort's tables (and, with FRONT_ROUTE, the
+// top-k) for the kernels after them, so no sort (or routing) launch precedes
+// them.
 bool gemm1_sorts_supported(int T, int variant);
+bool gemm1_routes_supported(int T, int variant);
+bool gemm1_wide_sorts_supported(int T);
+hipError_t launch_gemm1_wide_sorting(const Plan& p, const uint8_t* hs, const float* hs_scale,
+                                     const uint8_t* w1, const float* w1s, int bm2, hipStream_t s);
 hipError_t launch_gemm1_front(const Plan& p, const uint8_t* hs, const float* hs_scale,
                               const uint8_t* w1, const float* w1s, int variant, int front,
                               const FrontArgs& fa, hipStream_t s);

@@ -243,15 +243,22 @@ static void launch_stream1(const Plan& p, const uint8_t* hs, const float* hs_sca
                        p, hs, hs_scale, w1, w1s, fa);
 }
 
-bool gemm1_sorts_supported(int T, int variant) {
+bool gemm1_routes_supported(int T, int variant) {
     return (variant == 16 || variant == 5) && T > 0 && T <= SMALL_T;
+}
+
+bool gemm1_sorts_supported(int T, int variant) {
+    return gemm1_routes_supported(T, variant) || (variant == 15 && gemm1_wide_sorts_supported(T));
 }
 
 hipError_t launch_gemm1_front(const Plan& p, const uint8_t* hs, const float* hs_scale,
                               const uint8_t* w1, const float* w1s, int variant, int front,
                               const FrontArgs& fa, hipStream_t s) {
     if (p.T <= 0) return hipSuccess;
-    if (!gemm1_sorts_supported(p.T, variant)) return hipErrorInvalidValue;
+    if (front == FRONT_ROUTE ? !gemm1_routes_supported(p.T, variant)
+                             : !gemm1_sorts_supported(p.T, variant))
+        return hipErrorInvalidValue;
+    if (variant == 15) return launch_gemm1_wide_sorting(p, hs, hs_scale, w1, w1s, fa.bm2, s);
     if (front == FRONT_ROUTE) {
         if (variant == 5) launch_stream1<1, 4, 1, 1, FRONT_ROUTE>(p, hs, hs_scale, w1, w1s, s, fa);
         else launch_stream1<1, 2, 1, 4, FRONT_ROUTE>(p, hs, hs_scale, w1, w1s, s, fa);

@@ -19,10 +19,18 @@
 // All loads are ordinary compiler-visible loads, so the compiler's memory
 // counters stay exact and a load waits only for its own data.
 //
+// With SORT (T <= 256) the kernel also stands in for the sort launch: each
+// of its 4 waves ballots one 64-token chunk of the top-k ids per local expert
+// into LDS, every wave derives the expert counts, the bit-plane prefixes and
+// the workgroup's row tile from those ballots, and a row's token is the n-th
+// set bit of its expert's ballot in the right chunk. Workgroup (0, 0) writes
+// the sort's tables for GEMM2 and the combine.
+//
 // Operand layout as in the stream kernel: lane l feeds row (l % 16) of a
 // 16x128 operand with bytes [16g, 16g+16) and [64+16g, 64+16g+16) of the
 // k-block, g = l / 16. LDS rows are 128 bytes with chunk c of row r at
 // position c ^ swz8(r).
+#include "sort_impl.hpp"
 #include "tile_common.hpp"
 
 namespace mimoe {
@@ -34,11 +42,12 @@ constexpr int WIDE_NW = 4;                  // waves per workgroup
 constexpr int WIDE_G = 16 * WIDE_NW;        // gate columns per workgroup
 constexpr int WIDE_BM = 64;                 // rows per workgroup (see the launcher)
 
-template <int MTW, int D, int DA>
+template <int MTW, int D, int DA, bool SORT = false>
 __global__ __launch_bounds__(64 * WIDE_NW) void gemm1_wide_kernel(Plan p, const uint8_t* __restrict__ hs,
                                                                   const float* __restrict__ hs_scale,
                                                                   const uint8_t* __restrict__ w1,
-                                                                  const float* __restrict__ w1s) {
+                                                                  const float* __restrict__ w1s,
+                                                                  int bm2) {
     constexpr int BM = 16 * MTW;
     constexpr int THREADS = 64 * WIDE_NW;
     constexpr int ROWS_PER_PASS = THREADS / 8;  // 8 threads x 16 B cover one 128-byte row
@@ -48,13 +57,113 @@ __global__ __launch_bounds__(64 * WIDE_NW) void gemm1_wide_kernel(Plan p, const 
     __shared__ __attribute__((aligned(16))) uint8_t a_lds[2][BM * BLK];
     __shared__ float sa_lds[HB][BM];  // activation scales of the tile's rows, all k-blocks
     __shared__ __attribute__((aligned(16))) float cs_lds[2][2][BM];  // [buffer][gate, up][row]
-
-    int e, row0, nrows;
-    if (!find_tile(p.meta, META_MTILE1, blockIdx.y, BM, e, row0, nrows)) return;
+    // SORT: token ballots per (64-token chunk, local expert), and the first
+    // slot of each (chunk, expert) for the table writes
+    __shared__ unsigned long long s_bal[SORT ? WIDE_NW : 1][EL];
+    __shared__ int s_base[SORT ? WIDE_NW : 1][EL];
 
     const int tid = threadIdx.x;
     const int lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    static_assert(THREADS % BM == 0, "scale loader row");
+
+    // Row tile, and the tokens of this thread's loader rows and scale row.
+    int e, row0, nrows;
+    int tok_a[A_LD], tok_s;
+    if constexpr (SORT) {
+        static_assert(WIDE_NW * 64 >= 256 && BM == 64, "4 chunks of 64 tokens, 64-row tiles");
+        const int t = wave * 64 + lane;
+        uint32_t m = 0;
+        if (t < p.T) {
+            const int4 i0 = reinterpret_cast<const int4*>(p.topk_ids + (size_t)t * TOPK)[0];
+            const int4 i1 = reinterpret_cast<const int4*>(p.topk_ids + (size_t)t * TOPK)[1];
+            const int ids[TOPK] = {i0.x, i0.y, i0.z, i0.w, i1.x, i1.y, i1.z, i1.w};
+#pragma unroll
+            for (int k = 0; k < TOPK; ++k) {
+                const int l = ids[k] - p.local_offset;
+                m |= (unsigned)l < (unsigned)EL ? (1u << l) : 0u;
+            }
+        }
+#pragma unroll
+        for (int x = 0; x < EL; ++x) {
+            const unsigned long long bal = __ballot((m >> x) & 1u);
+            if (lane == x) s_bal[wave][x] = bal;
+        }
+        __syncthreads();
+        // lane x < 32: expert x's count over the chunks; prefixes as in wave_tile
+        unsigned long long b[WIDE_NW];
+        int cnt = 0;
+#pragma unroll
+        for (int c = 0; c < WIDE_NW; ++c) {
+            b[c] = s_bal[c][lane & (EL - 1)];
+            cnt += __popcll(b[c]);
+        }
+        if (lane >= EL) cnt = 0;
+        const int tiles = (cnt + BM - 1) / BM;
+        const int v0 = excl_prefix_small<9>(cnt) + cnt;
+        const int v1 = excl_prefix_small(tiles) + tiles;
+        if (blockIdx.x == 0 && blockIdx.y == 0) {
+            // the sort's tables: expert offsets, both tile prefixes, slots
+            const int t2 = (cnt + bm2 - 1) / bm2;
+            const int o2 = excl_prefix_small(t2);
+            if (lane < EL) {
+                if (wave == 0) {
+                    p.meta[META_EXPERT_OFF + lane] = v0 - cnt;
+                    p.meta[META_MTILE1 + lane] = v1 - tiles;
+                    p.meta[META_MTILE2 + lane] = o2;
+                    if (lane == EL - 1) {
+                        p.meta[META_EXPERT_OFF + EL] = v0;
+                        p.meta[META_MTILE1 + EL] = v1;
+                        p.meta[META_MTILE2 + EL] = o2 + t2;
+                    }
+                }
+                int base = v0 - cnt;
+#pragma unroll
+                for (int c = 0; c < WIDE_NW; ++c) base += c < wave ? __popcll(b[c]) : 0;
+                s_base[wave][lane] = base;
+            }
+            const TokLocal tl = load_local(p.topk_ids, p.topk_w, t, t < p.T, p.local_offset);
+            place_with_prefix(p, t, t < p.T, tl, s_base, lane, wave);
+        }
+        const int mt = blockIdx.y;
+        if (mt >= __builtin_amdgcn_readlane(v1, EL - 1)) return;  // the same for every wave
+        const int ee = __popcll(__ballot(lane < EL && v1 <= mt));
+        const int tfirst = __builtin_amdgcn_readlane(v1 - tiles, ee);
+        const int sfirst = __builtin_amdgcn_readlane(v0 - cnt, ee);
+        const int ce = __builtin_amdgcn_readlane(cnt, ee);
+        e = ee;
+        const int rank0 = (mt - tfirst) * BM;
+        row0 = sfirst + rank0;
+        nrows = min(BM, ce - rank0);
+        unsigned long long eb[WIDE_NW];
+#pragma unroll
+        for (int c = 0; c < WIDE_NW; ++c) eb[c] = s_bal[c][ee];
+        // token of tile row `row`: the (rank0 + row)-th token of expert ee
+        auto row_token = [&](int row) __attribute__((always_inline)) {
+            int k = rank0 + min(row, nrows - 1);
+            int chunk = 0;
+            unsigned long long bc = eb[0];
+#pragma unroll
+            for (int c = 0; c < WIDE_NW - 1; ++c) {
+                const int cc = __popcll(eb[c]);
+                if (chunk == c && k >= cc) {
+                    k -= cc;
+                    chunk = c + 1;
+                    bc = eb[c + 1];
+                }
+            }
+            return chunk * 64 + nth_set_bit(bc, k);
+        };
+#pragma unroll
+        for (int i = 0; i < A_LD; ++i) tok_a[i] = row_token((tid >> 3) + ROWS_PER_PASS * i);
+        tok_s = row_token(tid % BM);
+    } else {
+        if (!find_tile(p.meta, META_MTILE1, blockIdx.y, BM, e, row0, nrows)) return;
+#pragma unroll
+        for (int i = 0; i < A_LD; ++i)
+            tok_a[i] = p.sorted_tok[row0 + min((tid >> 3) + ROWS_PER_PASS * i, nrows - 1)];
+        tok_s = p.sorted_tok[row0 + min(tid % BM, nrows - 1)];
+    }
     const int jb = blockIdx.x * WIDE_G;  // first gate column of the workgroup
     const int j0 = jb + wave * 16;       // first gate column of this wave
     const int r = lane & 15, g = lane >> 4;
@@ -73,7 +182,7 @@ __global__ __launch_bounds__(64 * WIDE_NW) void gemm1_wide_kernel(Plan p, const 
 #pragma unroll
     for (int i = 0; i < A_LD; ++i) {
         const int row = (tid >> 3) + ROWS_PER_PASS * i;
-        a_src[i] = hs + (size_t)p.sorted_tok[row0 + min(row, nrows - 1)] * H + ac * 16;
+        a_src[i] = hs + (size_t)tok_a[i] * H + ac * 16;
         a_dst[i] = row * BLK + ((ac ^ swz8(row)) << 4);
     }
 
@@ -136,8 +245,8 @@ __global__ __launch_bounds__(64 * WIDE_NW) void gemm1_wide_kernel(Plan p, const 
     // Activation scales of every k-block into LDS once: in the loop they come
     // from LDS, so no vector load there waits on anything but its own data.
     for (int i = tid; i < HB * BM; i += THREADS) {
-        const int kb = i / BM, m = i % BM;
-        sa_lds[kb][m] = hs_scale[(size_t)kb * p.T + p.sorted_tok[row0 + min(m, nrows - 1)]];
+        const int kb = i / BM, m = i % BM;  // m == tid % BM: the row of tok_s
+        sa_lds[kb][m] = hs_scale[(size_t)kb * p.T + tok_s];
     }
     __syncthreads();
 
@@ -203,7 +312,22 @@ hipError_t launch_gemm1_wide(const Plan& p, const uint8_t* hs, const float* hs_s
     // 4- to 8-deep rings, more resident waves beat deeper rings here.
     dim3 grid(I / WIDE_G, max_mtiles(p.T, WIDE_BM));
     hipLaunchKernelGGL((gemm1_wide_kernel<WIDE_BM / 16, 2, 1>), grid, dim3(64 * WIDE_NW), 0, s,
-                       p, hs, hs_scale, w1, w1s);
+                       p, hs, hs_scale, w1, w1s, 0);
+    return hipGetLastError();
+}
+
+// Largest T the sorting wide kernel takes (4 waves x 64 tokens).
+constexpr int WIDE_SORT_MAX_T = 64 * WIDE_NW;
+
+bool gemm1_wide_sorts_supported(int T) { return T > 0 && T <= WIDE_SORT_MAX_T; }
+
+hipError_t launch_gemm1_wide_sorting(const Plan& p, const uint8_t* hs, const float* hs_scale,
+                                     const uint8_t* w1, const float* w1s, int bm2, hipStream_t s) {
+    if (p.T <= 0) return hipSuccess;
+    if (p.T > WIDE_SORT_MAX_T) return hipErrorInvalidValue;
+    dim3 grid(I / WIDE_G, max_mtiles(p.T, WIDE_BM));
+    hipLaunchKernelGGL((gemm1_wide_kernel<WIDE_BM / 16, 2, 1, true>), grid, dim3(64 * WIDE_NW), 0,
+                       s, p, hs, hs_scale, w1, w1s, bm2);
     return hipGetLastError();
 }
 

@@ -81,12 +81,13 @@ __device__ __forceinline__ int scan_counts(const Plan& p, int lane, int c, int b
     return v0 - own0;
 }
 
-// Exclusive prefix sum over the lanes of the wave of x in [0, 128): one
+// Exclusive prefix sum over the lanes of the wave of x in [0, 2^BITS): one
 // ballot per bit plane, counted below the lane with mbcnt (no LDS traffic).
+template <int BITS = 7>
 __device__ __forceinline__ int excl_prefix_small(int x) {
     int s = 0;
 #pragma unroll
-    for (int k = 0; k < 7; ++k) {
+    for (int k = 0; k < BITS; ++k) {
         const unsigned long long b = __ballot((x >> k) & 1);
         const uint32_t below = __builtin_amdgcn_mbcnt_hi(
             (uint32_t)(b >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)b, 0u));
@@ -147,6 +148,44 @@ __device__ inline void sort_one_wave(const Plan& p, const int* ids_base, const f
     }
     if (valid)
         for (; j < TOPK; ++j) p.tok_slot[(size_t)lane * TOPK + j] = -1;
+}
+
+// Writes the slots of one chunk given wcnt[wave][e] = first slot of expert e
+// for the wave's tokens (every thread of the workgroup calls it). Lane e
+// keeps expert e's token ballot and first slot; each token then walks its
+// own (at most 8) local experts in top-k order and fetches those with lane
+// shuffles, so no LDS read or weight search sits inside a per-expert loop.
+// A slot's place in the token's list is the number of its local experts
+// below it (ascending local expert order).
+__device__ __forceinline__ void place_with_prefix(const Plan& p, int t, bool valid,
+                                                  const TokLocal& tl, int (*wcnt)[EL], int lane,
+                                                  int wave) {
+    uint32_t bal_lo = 0, bal_hi = 0;
+#pragma unroll
+    for (int e = 0; e < EL; ++e) {
+        const unsigned long long bal = __ballot((tl.m >> e) & 1u);
+        if (lane == e) { bal_lo = (uint32_t)bal; bal_hi = (uint32_t)(bal >> 32); }
+    }
+    const int base_e = wcnt[wave][lane & (EL - 1)];
+    const uint32_t lower_lo = lane >= 32 ? 0xffffffffu : (1u << lane) - 1u;
+    const uint32_t lower_hi = lane >= 32 ? (1u << (lane - 32)) - 1u : 0u;
+#pragma unroll
+    for (int k = 0; k < TOPK; ++k) {
+        const int l = tl.lid[k];
+        const int src = l < 0 ? 0 : l;
+        const uint32_t blo = (uint32_t)__shfl((int)bal_lo, src);
+        const uint32_t bhi = (uint32_t)__shfl((int)bal_hi, src);
+        const int base = __shfl(base_e, src);
+        if (l >= 0) {
+            const int pos = base + __popc(blo & lower_lo) + __popc(bhi & lower_hi);
+            const int j = __popc(tl.m & ((1u << l) - 1u));
+            p.sorted_tok[pos] = t;
+            p.sorted_w[pos] = tl.lw[k];
+            p.tok_slot[(size_t)t * TOPK + j] = pos;
+        }
+    }
+    if (valid)
+        for (int j = __popc(tl.m); j < TOPK; ++j) p.tok_slot[(size_t)t * TOPK + j] = -1;
 }
 
 // Position of the k-th set bit (k counted from 0) of a 64-bit mask; k must be
