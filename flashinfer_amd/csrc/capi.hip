@@ -6,8 +6,8 @@
 // route -> sort -> GEMM1+SwiGLU -> GEMM2 -> combine on the caller's stream
 // with grids sized from T alone: no device-to-host copy, no host sync
 // (the reference syncs three times, kernel.py:572, :718, :773). Routing and
-// the sort fold into GEMM1 at T = 1, the sort alone up to T = 64 and from
-// T = 129 to 256 (the stream and wide GEMM1 kernels); see pick_front.
+// the sort fold into GEMM1 at T = 1, the sort alone up to T = 256 (the
+// stream GEMM1 kernels up to 64, the wide one above); see pick_front.
 #include <math.h>
 #include <stdarg.h>
 #include <stdio.h>
@@ -140,7 +140,8 @@ Variants pick_variants(int64_t T) {
     if (T <= 1) v = {5, VARIANT_GEMM2_COMBINE_KS};
     else if (T <= 4) v = {16, VARIANT_GEMM2_COMBINE_KS};
     else if (T <= 32) v = {16, 5};
-    else if (T <= 128) v = {16, 14};
+    else if (T <= 64) v = {16, 14};
+    else if (T <= 128) v = {15, 14};  // the wide GEMM1 folds in the sort from T = 65
     else if (T <= 192) v = {15, 13};
     else if (T <= 256) v = {15, 15};
     else if (T <= 1536) v = {15, 3};

@@ -324,13 +324,14 @@ def _sort_tables(T):
 @pytest.mark.parametrize("T,offset,skew", [(1, 0, False), (3, 32, True), (4, 0, False),
                                            (9, 0, False), (16, 96, False), (33, 224, False),
                                            (64, 0, False), (64, 32, True), (48, 256, False),
+                                           (65, 0, False), (100, 32, True), (128, 224, False),
                                            (129, 0, False), (200, 96, False), (256, 32, True),
                                            (160, 256, False)])
 def test_sort_in_gemm1_matches_sort_launch(T, offset, skew, monkeypatch):
     """GEMM1 finding its row tiles from the top-k ids (and writing the sort's
     tables itself) gives bit-identical output and tables to the separate sort
     launch, for every GEMM1 kernel that can do it (single-wave workgroups at
-    T = 1, K split up to 64, the wide 64-row tiles from 129 to 256): ragged T,
+    T = 1, K split up to 64, the wide 64-row tiles from 65 to 256): ragged T,
     other shard offsets, several row tiles per expert (skew) and no local
     token at all (offset 256)."""
     from flashinfer_amd import _lib, kernel
