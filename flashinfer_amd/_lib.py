@@ -27,6 +27,7 @@ MI_MOE_ERR_WORKSPACE = 2
 MI_MOE_ERR_HIP = 3
 MI_MOE_DTYPE_BF16 = 0
 MI_MOE_DTYPE_F32 = 1
+MI_MOE_MAX_TOKENS = 131072  # largest num_tokens the library accepts
 
 EXPORTED = ("mi_moe_workspace_size", "mi_moe_workspace_layout", "mi_moe_run",
             "mi_moe_run_profiled", "mi_moe_run_bf16", "mi_moe_route", "mi_moe_sort", "mi_moe_quantize_fp8",

@@ -35,7 +35,12 @@ int fail(int code, const char* fmt, ...) {
     return code;
 }
 
-constexpr int64_t kMaxTokens = 1 << 22;  // keeps every slot index below 2^31
+// The LDS-tiled GEMMs address gathered rows with 32-bit byte offsets (token
+// * H into hidden_states, slot * 2I into the bf16 activations, with at most
+// 8 slots per token), so T is capped where those stay below 2^32.
+constexpr int64_t kMaxTokens = MI_MOE_MAX_TOKENS;
+static_assert((uint64_t)kMaxTokens * H <= (1ull << 32), "GEMM1 tile row offsets fit 32 bits");
+static_assert((uint64_t)kMaxTokens * TOPK * I * 2 <= (1ull << 32), "GEMM2 tile row offsets fit 32 bits");
 
 size_t align_up(size_t x) { return (x + 255) & ~(size_t)255; }
 

@@ -34,6 +34,10 @@ extern "C" {
 #define MI_MOE_DTYPE_BF16 0
 #define MI_MOE_DTYPE_F32 1
 
+/* Largest num_tokens any entry point accepts (larger T is MI_MOE_ERR_INVALID):
+ * the row-gathering GEMM kernels keep byte offsets in 32 bits. */
+#define MI_MOE_MAX_TOKENS 131072
+
 /* Arguments of one call. Field order and meaning follow the reference entry
  * point solution/triton/kernel.py:600-613 (run(routing_logits, routing_bias,
  * hidden_states, hidden_states_scale, gemm1_weights, gemm1_weights_scale,
@@ -52,7 +56,7 @@ typedef struct mi_moe_args {
     int64_t local_expert_offset;       /* first global expert id of this shard */
     float routed_scaling_factor;
     void* output;                      /* bf16 [T, 7168], fully overwritten */
-    int64_t num_tokens;                /* T >= 0 */
+    int64_t num_tokens;                /* 0 <= T <= MI_MOE_MAX_TOKENS */
     int32_t bias_dtype;                /* MI_MOE_DTYPE_* */
     int32_t reserved;                  /* must be 0 */
     void* workspace;                   /* >= mi_moe_workspace_size(T) bytes, 256-B aligned */

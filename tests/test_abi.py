@@ -99,6 +99,13 @@ def test_run_rejects_before_launch():
     assert b"aligned" in L.mi_moe_last_error()
     assert _call(_args(workspace_bytes=100)) == _lib.MI_MOE_ERR_WORKSPACE
     assert b"workspace" in L.mi_moe_last_error()
+    # the largest T whose gathered-row offsets fit the tile GEMMs' 32 bits
+    big = _lib.MI_MOE_MAX_TOKENS
+    assert _call(_args(num_tokens=big + 1)) == _lib.MI_MOE_ERR_INVALID
+    assert b"out of range" in L.mi_moe_last_error()
+    lay = _lib.MiMoeLayout()
+    assert L.mi_moe_workspace_layout(big, ctypes.byref(lay)) == _lib.MI_MOE_OK
+    assert L.mi_moe_workspace_layout(big + 1, ctypes.byref(lay)) == _lib.MI_MOE_ERR_INVALID
     # T == 0 is a valid no-op
     assert _call(_args(num_tokens=0)) == _lib.MI_MOE_OK
     assert L.mi_moe_last_error() == b""
@@ -211,3 +218,12 @@ def test_unbuilt_shape_is_refused():
         _lib.lib((2048, 768))
     with pytest.raises(ValueError, match="H % 1024"):
         _lib.lib((7000, 2048))
+
+
+def test_header_constants_match_bindings():
+    """The Python mirror's constants are the header's #defines."""
+    hdr = open(os.path.join(os.path.dirname(__file__), "..", "include", "mi_moe.h")).read()
+    defs = dict(re.findall(r"#define (MI_MOE_[A-Z0-9_]+) (\d+)", hdr))
+    for name in ("MI_MOE_OK", "MI_MOE_ERR_INVALID", "MI_MOE_ERR_WORKSPACE", "MI_MOE_ERR_HIP",
+                 "MI_MOE_DTYPE_BF16", "MI_MOE_DTYPE_F32", "MI_MOE_MAX_TOKENS"):
+        assert int(defs[name]) == getattr(_lib, name), name
