@@ -185,6 +185,26 @@ def test_skew_all_rows_on_biased_experts():
     assert torch.equal(eoff, want)
 
 
+def test_max_tokens_every_slot_local():
+    """The largest accepted batch with every token routed to the same 8 local
+    experts: S = 8T = 2^20 slots, so the last slots' gathered-row offsets are
+    the largest the tile GEMMs form (just under 2^32 bytes). Expert offsets
+    are exact, and the first and last tokens (the extreme slots of each
+    expert) and a spread between them match the oracle."""
+    from flashinfer_amd import _lib, kernel
+    T = _lib.MI_MOE_MAX_TOKENS
+    log(f"test_max_tokens_every_slot_local[T={T}]: generating inputs")
+    wl = W.make_workload("max_tokens_skew", T, 113, skew=True)
+    log("test_max_tokens_every_slot_local: running")
+    out = run_gpu(wl, fill=float("nan"))
+    L = _lib.workspace_layout(T)
+    eoff = kernel.last_workspace()[L.expert_off:L.expert_off + 33 * 4].view(torch.int32).cpu()
+    want = torch.tensor([min(e, 8) * T for e in range(33)], dtype=torch.int32)
+    assert torch.equal(eoff, want)
+    tokens = torch.cat([torch.tensor([0, 1, T - 2, T - 1]), spread_tokens(T, 12)]).unique()
+    _check_output(wl, out, tokens)
+
+
 def _random_workloads(n=20, seed=2026):
     """Seeded (T, offset, skew, routed_scaling_factor) draws: ragged T from 1
     to ~1100 (weighted to decode sizes), shard offsets that are negative,
