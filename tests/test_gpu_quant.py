@@ -105,12 +105,12 @@ def test_quantize_rejects_bad_arguments():
     assert q.shape == (0, H) and s.shape == (H // 128, 0)
 
 
-@pytest.mark.parametrize("T", [1, 4, 16, 64, 300, 1500])
+@pytest.mark.parametrize("T", [1, 4, 16, 64, 100, 200, 300, 1500])
 def test_run_bf16_matches_quantize_then_run(T):
     """run_bf16 (quantiser and routing in one launch, then the layer) writes
     the fp8 pair of quantize_activations and the output of run on it, bit for
-    bit, through each front end (T=1..64 sort in GEMM1, 300 sort kernel,
-    1500 chunked sort)."""
+    bit, through each front end (T=1..64 sort in the stream GEMM1, 100 and
+    200 in the wide GEMM1, 300 sort kernel, 1500 chunked sort)."""
     from flashinfer_amd import kernel
     from _helpers import gpu_args
     log(f"test_run_bf16_matches_quantize_then_run[T={T}]")
