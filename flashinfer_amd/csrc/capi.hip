@@ -144,7 +144,7 @@ Variants pick_variants(int64_t T) {
     // busy with fewer than 4 row tiles): one launch fewer where launches dominate
     if (T <= 1) v = {5, VARIANT_GEMM2_COMBINE_KS};
     else if (T <= 4) v = {16, VARIANT_GEMM2_COMBINE_KS};
-    else if (T <= 32) v = {16, 5};
+    else if (T <= 8) v = {16, 5};
     else if (T <= 64) v = {16, 14};
     else if (T <= 128) v = {15, 14};  // the wide GEMM1 folds in the sort from T = 65
     else if (T <= 192) v = {15, 13};
