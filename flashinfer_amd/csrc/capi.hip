@@ -147,7 +147,7 @@ Variants pick_variants(int64_t T) {
     else if (T <= 8) v = {16, 5};
     else if (T <= 64) v = {16, 14};
     else if (T <= 128) v = {15, 14};  // the wide GEMM1 folds in the sort from T = 65
-    else if (T <= 192) v = {15, 13};
+    else if (T <= 176) v = {15, 13};  // wide GEMM2 ahead by 3.5 us at T = 192, behind by ~2 at 160
     else if (T <= 256) v = {15, 15};
     else if (T <= 1536) v = {15, 3};
     else v = {3, 3};
