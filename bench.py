@@ -340,13 +340,28 @@ def measured_peaks():
     return out
 
 
+def profiler_inherited(env=None) -> bool:
+    """True when this process runs under a profiler: rocprofv3 preloads its
+    tool library (LD_PRELOAD, ROCP_TOOL_LIBRARIES), which initialises the GPU
+    before the program starts, so no child may be started from here."""
+    env = os.environ if env is None else env
+    if env.get("ROCP_TOOL_LIBRARIES") or env.get("HSA_TOOLS_LIB"):
+        return True
+    preload = env.get("LD_PRELOAD", "")
+    return any(k in preload for k in ("rocprof", "roctracer", "rocprofiler"))
+
+
 def pmc_traffic(workload, kernel_key, copy_mib=1024, timeout=180):
     """HBM bytes per launch of the first kernel whose name contains
     ``kernel_key``, from two rocprofv3 counter passes (FETCH_SIZE, then
     WRITE_SIZE) over a short child run of this bench. Each pass also times a
     device copy of ``copy_mib`` MiB, whose counter reading gives the scale
-    from counter units to bytes. Returns None if rocprofv3 is unavailable or
-    a pass fails. Must run before this process touches the GPU."""
+    from counter units to bytes. Returns None, starting nothing, if rocprofv3
+    is unavailable or this process itself runs under a profiler; None if a
+    pass fails. Must run before this process touches the GPU."""
+    if profiler_inherited():
+        log("[bench] running under a profiler: counter passes skipped (traffic = null)")
+        return None
     exe = shutil.which("rocprofv3")
     if exe is None:
         return None

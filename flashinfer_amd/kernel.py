@@ -42,7 +42,26 @@ def _workspace_cache() -> dict:
     return c
 
 
+# Workspaces recorded into captured HIP graphs. A graph replays into the
+# addresses it captured, so every capture gets a buffer of its own (graphs
+# replayed on two streams never share one), allocated inside the capture (from
+# the graph's memory pool) and referenced here until the process ends, so no
+# later allocation, of this module or of the pool, can be handed its memory.
+_CAPTURED: list = []
+_IS_CAPTURING = getattr(torch._C, "_cuda_isCurrentStreamCapturing", None)
+
+
+def _capturing() -> bool:
+    if _IS_CAPTURING is not None:
+        return bool(_IS_CAPTURING())
+    return torch.cuda.is_current_stream_capturing()
+
+
 def _workspace(device: torch.device, stream: int, nbytes: int) -> torch.Tensor:
+    if _capturing():
+        ws = torch.empty(max(nbytes, 256), dtype=torch.uint8, device=device)
+        _CAPTURED.append(ws)
+        return ws
     key = (device.index, stream)
     _workspaces = _workspace_cache()
     ws = _workspaces.get(key)

@@ -29,3 +29,25 @@ def test_algorithmic_constants():
     # per-launch GEMM bytes: weights once per active expert, one row in and out per slot
     assert bench.gemm1_bytes(105, 20) == 20 * 29_367_296 + 105 * (7168 + 224 + 4096)
     assert bench.gemm2_bytes(105, 20) == 20 * 14_683_648 + 105 * (4096 + 14336)
+
+
+def test_counter_passes_never_start_under_a_profiler(monkeypatch):
+    """Run under rocprofv3 (its tool library preloaded), bench.py must not
+    start its own rocprofv3 children: the profiler has already initialised
+    the GPU in this process. pmc_traffic returns None without spawning."""
+    started = []
+    monkeypatch.setattr(bench.subprocess, "run", lambda *a, **k: started.append(a) or None)
+    monkeypatch.setattr(bench.shutil, "which", lambda name: "/opt/rocm/bin/" + name)
+    for env in ({"LD_PRELOAD": "/opt/rocm/lib/rocprofiler-sdk/librocprofiler-sdk-tool.so"},
+                {"ROCP_TOOL_LIBRARIES": "/opt/rocm/lib/rocprofiler-sdk/librocprofiler-sdk-tool.so"},
+                {"LD_PRELOAD": "/x/libharness.so:/opt/rocm/lib/librocprofiler-sdk.so"}):
+        for k in ("LD_PRELOAD", "ROCP_TOOL_LIBRARIES", "HSA_TOOLS_LIB"):
+            monkeypatch.delenv(k, raising=False)
+        for k, v in env.items():
+            monkeypatch.setenv(k, v)
+        assert bench.profiler_inherited()
+        assert bench.pmc_traffic("c3_t8192", "gemm1_tile") is None
+    assert started == []
+    # an unrelated preload is not a profiler
+    assert not bench.profiler_inherited({"LD_PRELOAD": "/usr/lib/libharness.so"})
+    assert not bench.profiler_inherited({})

@@ -80,13 +80,30 @@ def test_output_parity_mid(name):
     _check_output(wl, out, spread_tokens(wl.T, 256))
 
 
-@pytest.mark.parametrize("name", ["c3_t8192", "c4_t14000_skew"])
-def test_output_parity_large(name):
-    log(f"test_output_parity_large[{name}]")
-    wl = W.standard(name)
+def test_output_parity_prefill_every_token():
+    """T=8192: every token against the oracle (11,559 slots over 28 experts,
+    each expert spanning several 256-row tiles with a partial last one), so a
+    mis-indexed row tile or tile order shows up wherever it lands."""
+    log("test_output_parity_prefill_every_token[c3_t8192]")
+    wl = W.standard("c3_t8192")
     out = run_gpu(wl, fill=float("nan"))
     assert torch.isfinite(out.float()).all()
-    _check_output(wl, out, spread_tokens(wl.T, 48))
+    _check_output(wl, out, torch.arange(wl.T))
+
+
+def test_output_parity_skew_tile_bands():
+    """T=14000 with every token on the same 8 local experts (14,000 rows each,
+    token-ascending): tokens 0..255 are each expert's whole first 256-row
+    tile, tokens 13824..13999 its partial last tile (176 rows), plus a spread
+    between them."""
+    log("test_output_parity_skew_tile_bands[c4_t14000_skew]")
+    wl = W.standard("c4_t14000_skew")
+    out = run_gpu(wl, fill=float("nan"))
+    assert torch.isfinite(out.float()).all()
+    T = wl.T
+    last = (T // 256) * 256
+    tokens = torch.cat([torch.arange(256), torch.arange(last, T), spread_tokens(T, 64)]).unique()
+    _check_output(wl, out, tokens)
 
 
 @pytest.mark.parametrize("name,fuse", [("c1_t1", "0"), ("c1_t4", "1"), ("c1_t16", "1"), ("c1_t16", "0"),
@@ -235,11 +252,12 @@ def test_random_workloads(i, T, offset, skew, rsf):
 
 
 # Both sides of every T at which the default kernels change: fused GEMM2+combine
-# (T <= 4), routing inside GEMM1 (T = 1), sort inside GEMM1 (T <= 64), streaming GEMM
-# shapes (32, 128), wide GEMM1 (> 128), wide GEMM2 (193..256), tiled GEMM2
-# (> 256), chunked two-kernel sort (> 1024), LDS-tiled GEMM1 (> 1536).
-@pytest.mark.parametrize("T", [1, 2, 4, 5, 8, 9, 32, 33, 64, 65, 128, 129, 192, 193, 256, 257, 1024,
-                               1025, 1536, 1537, 2049])
+# (T <= 4), routing inside GEMM1 (T = 1), sort inside GEMM1 (T <= 64), GEMM2 stream
+# shapes (8 / 9), wide GEMM1 with the sort folded in (65..256), GEMM2 stream shapes
+# (128 / 129), wide GEMM2 (177..256), tiled GEMM2 (> 256), chunked two-kernel sort
+# (> 1024), LDS-tiled GEMM1 (> 1536).
+@pytest.mark.parametrize("T", [1, 2, 4, 5, 8, 9, 32, 33, 64, 65, 128, 129, 176, 177, 192, 193, 256,
+                               257, 1024, 1025, 1536, 1537, 2049])
 def test_variant_boundaries(T):
     log(f"test_variant_boundaries[T={T}]")
     wl = W.make_workload(f"boundary_t{T}", T=T, seed=1000 + T, local_expert_offset=32 * (T % 8))

@@ -47,7 +47,7 @@ def test_graph_capture_and_replay(name, other):
     out = torch.empty(wl.T, H, dtype=torch.bfloat16, device="cuda")
     side = torch.cuda.Stream()
     side.wait_stream(torch.cuda.current_stream())
-    with torch.cuda.stream(side):  # warm up: workspace and code objects outside the capture
+    with torch.cuda.stream(side):  # warm up: code objects load outside the capture
         kernel.run(*static, out)
     torch.cuda.current_stream().wait_stream(side)
     torch.cuda.synchronize()
@@ -116,3 +116,56 @@ def test_two_threads_one_stream():
     for t in threads:
         t.join(timeout=120)
     assert not errors, errors
+
+
+def test_graphs_at_increasing_sizes_keep_their_workspaces():
+    """Two graphs captured one after the other, the second at a larger T, then
+    replayed in the opposite order and concurrently on two streams: each
+    capture owns its workspace, so every replay equals an eager call on the
+    same inputs (a shared, regrown workspace would leave the first graph
+    writing into freed memory, and concurrent replays would mix tables)."""
+    log("test_graphs_at_increasing_sizes_keep_their_workspaces")
+    wls = [W.standard("c1_t16"), W.standard("c1_t64")]
+    statics = [gpu_args(wl) for wl in wls]
+    outs = [torch.empty(wl.T, H, dtype=torch.bfloat16, device="cuda") for wl in wls]
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        for st, o in zip(statics, outs):
+            kernel.run(*st, o)
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    graphs = []
+    for st, o in zip(statics, outs):  # T = 16, then T = 64 (a larger workspace)
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g):
+            kernel.run(*st, o)
+        graphs.append(g)
+    torch.cuda.synchronize()
+    refs = []
+    for st, o in zip(statics, outs):
+        e = torch.empty_like(o)
+        kernel.run(*st, e)
+        refs.append(e)
+    torch.cuda.synchronize()
+    for rep in range(3):
+        for i in (1, 0):
+            outs[i].fill_(float("nan"))
+            graphs[i].replay()
+            torch.cuda.synchronize()
+            assert torch.equal(_bits(outs[i]), _bits(refs[i])), (rep, i)
+            # eager work of the program between replays
+            junk = torch.empty_like(outs[i])
+            kernel.run(*statics[i], junk)
+            torch.cuda.synchronize()
+    streams = [torch.cuda.Stream(), torch.cuda.Stream()]
+    for o in outs:
+        o.fill_(float("nan"))
+    torch.cuda.synchronize()
+    for g, s in zip(graphs, streams):
+        with torch.cuda.stream(s):
+            g.replay()
+    torch.cuda.synchronize()
+    for i in range(2):
+        assert torch.equal(_bits(outs[i]), _bits(refs[i])), ("concurrent", i)
+    del graphs
