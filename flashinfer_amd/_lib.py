@@ -28,10 +28,12 @@ MI_MOE_ERR_HIP = 3
 MI_MOE_DTYPE_BF16 = 0
 MI_MOE_DTYPE_F32 = 1
 MI_MOE_MAX_TOKENS = 131072  # largest num_tokens the library accepts
+MI_MOE_NOALLOC_MAX_TOKENS = 256  # largest num_tokens of mi_moe_run_noalloc
 
 EXPORTED = ("mi_moe_workspace_size", "mi_moe_workspace_layout", "mi_moe_run",
-            "mi_moe_run_profiled", "mi_moe_run_bf16", "mi_moe_route", "mi_moe_sort", "mi_moe_quantize_fp8",
-            "mi_moe_shape", "mi_moe_last_error", "mi_moe_version")
+            "mi_moe_run_profiled", "mi_moe_run_bf16", "mi_moe_run_noalloc", "mi_moe_route",
+            "mi_moe_sort", "mi_moe_quantize_fp8", "mi_moe_shape", "mi_moe_last_error",
+            "mi_moe_version")
 NUM_PHASES = 5
 PHASES = ("route", "sort", "gemm1_swiglu", "gemm2", "combine")
 
@@ -80,6 +82,8 @@ def _bind(L: ctypes.CDLL) -> None:
     L.mi_moe_workspace_layout.restype = ctypes.c_int
     L.mi_moe_run.argtypes = [ctypes.POINTER(MiMoeArgs), ctypes.c_void_p]
     L.mi_moe_run.restype = ctypes.c_int
+    L.mi_moe_run_noalloc.argtypes = [ctypes.POINTER(MiMoeArgs), ctypes.c_void_p]
+    L.mi_moe_run_noalloc.restype = ctypes.c_int
     L.mi_moe_run_bf16.argtypes = [ctypes.POINTER(MiMoeArgs), ctypes.c_void_p, ctypes.c_void_p]
     L.mi_moe_run_bf16.restype = ctypes.c_int
     L.mi_moe_run_profiled.argtypes = [ctypes.POINTER(MiMoeArgs), ctypes.c_void_p,

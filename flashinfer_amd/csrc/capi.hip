@@ -13,6 +13,8 @@
 #include <stdio.h>
 #include <stdlib.h>
 
+#include <atomic>
+#include <mutex>
 #include <string>
 
 #include "../../include/mi_moe.h"
@@ -42,10 +44,10 @@ constexpr int64_t kMaxTokens = MI_MOE_MAX_TOKENS;
 static_assert((uint64_t)kMaxTokens * H <= (1ull << 32), "GEMM1 tile row offsets fit 32 bits");
 static_assert((uint64_t)kMaxTokens * TOPK * I * 2 <= (1ull << 32), "GEMM2 tile row offsets fit 32 bits");
 
-size_t align_up(size_t x) { return (x + 255) & ~(size_t)255; }
+constexpr size_t align_up(size_t x) { return (x + 255) & ~(size_t)255; }
 
-mi_moe_layout make_layout(int64_t T) {
-    mi_moe_layout L;
+constexpr mi_moe_layout make_layout(int64_t T) {
+    mi_moe_layout L{};
     const size_t t = (size_t)(T < 0 ? 0 : T);
     const size_t s_max = 8 * t;
     size_t o = 0;
@@ -63,6 +65,55 @@ mi_moe_layout make_layout(int64_t T) {
 }
 
 bool aligned(const void* p, size_t a) { return ((uintptr_t)p % a) == 0; }
+
+// Scratch of the no-allocation entry point (mi_moe_run_noalloc): the
+// workspace of MI_MOE_NOALLOC_MAX_TOKENS tokens, one copy per GPU the library
+// runs on, held until the process ends. Host code never passes `scratch`
+// itself (on the host it names a stand-in, not device memory): it uses the
+// device address hipGetSymbolAddress returns for the device in question.
+constexpr size_t kScratchBytes = make_layout(MI_MOE_NOALLOC_MAX_TOKENS).total;
+static_assert(kScratchBytes % 256 == 0, "scratch is a whole number of 256-byte blocks");
+static __device__ __align__(256) uint8_t scratch[kScratchBytes];
+
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+std::atomic<void*> g_scratch_ptr[kMaxDevices];
+
+// Device address of `scratch` on the device `stream` belongs to, looked up
+// once per device (with that device current) and kept.
+int scratch_address(hipStream_t stream, void** out) {
+    int dev = -1;
+    hipError_t e = hipStreamGetDevice(stream, &dev);
+    if (e != hipSuccess)
+        return fail(MI_MOE_ERR_HIP, "mi_moe_run_noalloc: hipStreamGetDevice failed: %s",
+                    hipGetErrorString(e));
+    if (dev < 0 || dev >= kMaxDevices)
+        return fail(MI_MOE_ERR_INVALID, "mi_moe_run_noalloc: device %d beyond the %d supported",
+                    dev, kMaxDevices);
+    void* p = g_scratch_ptr[dev].load(std::memory_order_acquire);
+    if (p) {
+        *out = p;
+        return MI_MOE_OK;
+    }
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    p = g_scratch_ptr[dev].load(std::memory_order_relaxed);
+    if (!p) {
+        int cur = -1;
+        e = hipGetDevice(&cur);
+        if (e == hipSuccess && cur != dev) e = hipSetDevice(dev);
+        if (e == hipSuccess) e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        if (cur >= 0 && cur != dev) {
+            const hipError_t r = hipSetDevice(cur);
+            if (e == hipSuccess) e = r;
+        }
+        if (e != hipSuccess || !p)
+            return fail(MI_MOE_ERR_HIP, "mi_moe_run_noalloc: scratch address on device %d: %s",
+                        dev, hipGetErrorString(e));
+        g_scratch_ptr[dev].store(p, std::memory_order_release);
+    }
+    *out = p;
+    return MI_MOE_OK;
+}
 
 // Device pointers of one call into the caller's workspace.
 Plan make_plan(void* workspace, const mi_moe_layout& L, int64_t T, int64_t local_expert_offset,
@@ -388,6 +439,27 @@ int mi_moe_run_bf16(const mi_moe_args* a, const void* hidden_bf16, void* stream)
         return fail(MI_MOE_ERR_INVALID, "mi_moe_run_bf16: hidden_bf16 is NULL");
     }
     return run_impl(a, (hipStream_t)stream, nullptr, hidden_bf16);
+}
+
+int mi_moe_run_noalloc(const mi_moe_args* a, void* stream) {
+    g_last_error.clear();
+    if (!a) return fail(MI_MOE_ERR_INVALID, "mi_moe_run_noalloc: args is NULL");
+    if (a->workspace || a->workspace_bytes)
+        return fail(MI_MOE_ERR_INVALID,
+                    "mi_moe_run_noalloc: workspace must be NULL and workspace_bytes 0 (the "
+                    "library's per-GPU scratch holds the intermediates)");
+    if (a->num_tokens > MI_MOE_NOALLOC_MAX_TOKENS)
+        return fail(MI_MOE_ERR_INVALID,
+                    "mi_moe_run_noalloc: num_tokens %lld exceeds MI_MOE_NOALLOC_MAX_TOKENS (%d); "
+                    "use mi_moe_run with a workspace",
+                    (long long)a->num_tokens, MI_MOE_NOALLOC_MAX_TOKENS);
+    void* ws = nullptr;
+    const int rc = scratch_address((hipStream_t)stream, &ws);
+    if (rc != MI_MOE_OK) return rc;
+    mi_moe_args b = *a;
+    b.workspace = ws;
+    b.workspace_bytes = kScratchBytes;
+    return run_impl(&b, (hipStream_t)stream, nullptr);
 }
 
 int mi_moe_run_profiled(const mi_moe_args* a, void* stream, void* const* events, int32_t n_events) {

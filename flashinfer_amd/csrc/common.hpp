@@ -141,7 +141,9 @@ hipError_t launch_route(const float* logits, const void* bias, int bias_is_f32, 
 hipError_t launch_sort(const Plan& p, int bm1, int bm2, hipStream_t s);
 // Routing + sort in one single-workgroup launch (small T only).
 bool route_sort_supported(int T);
-int sort_chunks(int T);
+// Tokens per chunk of the large-T sort (one 1024-thread workgroup each).
+constexpr int SORT_CHUNK = 1024;
+constexpr int sort_chunks(int T) { return (T + SORT_CHUNK - 1) / SORT_CHUNK; }
 hipError_t launch_route_sort(const Plan& p, const float* logits, const void* bias, int bias_is_f32,
                              int bm1, int bm2, hipStream_t s);
 hipError_t launch_gemm1(const Plan& p, const uint8_t* hs, const float* hs_scale, const uint8_t* w1,

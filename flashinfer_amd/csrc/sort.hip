@@ -27,7 +27,7 @@
 
 namespace mimoe {
 
-constexpr int CHUNK = 1024;
+constexpr int CHUNK = SORT_CHUNK;
 
 // Per-wave hit counts of the chunk into wcnt[wave][e] (lane e writes).
 __device__ __forceinline__ void wave_counts(const TokLocal& tl, int lane, int wave,
@@ -178,8 +178,6 @@ __global__ __launch_bounds__(1024) void sort_place_kernel(Plan p, int nchunks, i
 }
 
 bool route_sort_supported(int T) { return T > 0 && T <= ROUTE_SORT_MAX_T; }
-
-int sort_chunks(int T) { return (T + CHUNK - 1) / CHUNK; }
 
 hipError_t launch_route_sort(const Plan& p, const float* logits, const void* bias, int bias_is_f32,
                              int bm1, int bm2, hipStream_t s) {

@@ -194,6 +194,65 @@ def run(
     return None
 
 
+def run_noalloc(routing_logits, routing_bias, hidden_states, hidden_states_scale, gemm1_weights,
+                gemm1_weights_scale, gemm2_weights, gemm2_weights_scale, local_expert_offset,
+                routed_scaling_factor, output):
+    """``run`` for callers that cannot allocate device memory (HIP graph
+    capture, serving loops): no workspace and no copies; the intermediates
+    live in the library's static per-GPU scratch (``mi_moe_run_noalloc``).
+    T is at most ``MI_MOE_NOALLOC_MAX_TOKENS`` (256) and every tensor must be
+    contiguous. Calls that overlap on one GPU share the scratch and must be
+    serialised. No counterpart in the reference."""
+    tensors = (routing_logits, routing_bias, hidden_states, hidden_states_scale, gemm1_weights,
+               gemm1_weights_scale, gemm2_weights, gemm2_weights_scale, output)
+    if not isinstance(routing_logits, torch.Tensor) or routing_logits.dim() != 2:
+        raise ValueError("routing_logits must be a 2-D tensor [T, 256]")
+    T = int(routing_logits.shape[0])
+    shape = _shape_of(gemm1_weights)
+    H, I = shape
+    _expect(routing_logits, "routing_logits", (torch.float32,), (T, E_GLOBAL))
+    _expect(routing_bias, "routing_bias", (torch.bfloat16, torch.float32), (E_GLOBAL,))
+    _expect(hidden_states, "hidden_states", (FP8,), (T, H))
+    _expect(hidden_states_scale, "hidden_states_scale", (torch.float32,), (H // BLOCK, T))
+    _expect(gemm1_weights, "gemm1_weights", (FP8,), (E_LOCAL, 2 * I, H))
+    _expect(gemm1_weights_scale, "gemm1_weights_scale", (torch.float32,),
+            (E_LOCAL, 2 * I // BLOCK, H // BLOCK))
+    _expect(gemm2_weights, "gemm2_weights", (FP8,), (E_LOCAL, H, I))
+    _expect(gemm2_weights_scale, "gemm2_weights_scale", (torch.float32,),
+            (E_LOCAL, H // BLOCK, I // BLOCK))
+    _expect(output, "output", (torch.bfloat16,), (T, H))
+    if T > _lib.MI_MOE_NOALLOC_MAX_TOKENS:
+        raise ValueError(f"run_noalloc takes at most {_lib.MI_MOE_NOALLOC_MAX_TOKENS} tokens, "
+                         f"got {T}; use run()")
+    device = output.device
+    if device.type != "cuda":
+        raise ValueError("run_noalloc() needs tensors on a ROCm GPU (device type 'cuda')")
+    for t in tensors:
+        if t.device != device:
+            raise ValueError("all tensors must be on the same device")
+        if not t.is_contiguous():
+            raise ValueError("run_noalloc() makes no copies: every tensor must be contiguous")
+    offset = _scalar(local_expert_offset, int)
+    rsf = _scalar(routed_scaling_factor, float)
+    if T == 0:
+        return None
+    L = _lib.lib(shape)
+    args = _lib.MiMoeArgs(
+        routing_logits=routing_logits.data_ptr(), routing_bias=routing_bias.data_ptr(),
+        hidden_states=hidden_states.data_ptr(), hidden_states_scale=hidden_states_scale.data_ptr(),
+        gemm1_weights=gemm1_weights.data_ptr(), gemm1_weights_scale=gemm1_weights_scale.data_ptr(),
+        gemm2_weights=gemm2_weights.data_ptr(), gemm2_weights_scale=gemm2_weights_scale.data_ptr(),
+        local_expert_offset=offset, routed_scaling_factor=rsf, output=output.data_ptr(),
+        num_tokens=T,
+        bias_dtype=(_lib.MI_MOE_DTYPE_BF16 if routing_bias.dtype == torch.bfloat16
+                    else _lib.MI_MOE_DTYPE_F32),
+        reserved=0, workspace=None, workspace_bytes=0)
+    with torch.cuda.device(device):
+        stream = torch.cuda.current_stream(device).cuda_stream
+        _lib.check(L.mi_moe_run_noalloc(ctypes.byref(args), ctypes.c_void_p(stream)), L)
+    return None
+
+
 @torch.no_grad()
 def run_profiled(*args, events):
     """``run`` that also records ``events`` (6 ``torch.cuda.Event`` with

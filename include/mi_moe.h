@@ -148,6 +148,24 @@ int mi_moe_quantize_fp8(const void* hidden_bf16, int64_t num_tokens, uint8_t* hi
  * from them; no counterpart in the reference. */
 int mi_moe_shape(int32_t* hidden_size, int32_t* intermediate_size);
 
+/* Largest num_tokens mi_moe_run_noalloc accepts. */
+#define MI_MOE_NOALLOC_MAX_TOKENS 256
+
+/* mi_moe_run without a caller workspace and without any allocation, for
+ * callers that cannot allocate device memory (code under HIP graph capture,
+ * tight serving loops, harnesses that forbid hipMalloc). No counterpart in
+ * the reference. args->workspace must be NULL and args->workspace_bytes 0:
+ * the intermediates live in the library's static device array (one per GPU,
+ * mi_moe_workspace_size(MI_MOE_NOALLOC_MAX_TOKENS) bytes, about 38 MB at
+ * H = 7168, I = 2048, held until the process ends), so num_tokens is at most
+ * MI_MOE_NOALLOC_MAX_TOKENS (larger T: MI_MOE_ERR_INVALID, nothing enqueued).
+ * The first call on a device looks up that array's address there. The
+ * kernels, results and every other check are those of mi_moe_run; the array
+ * keeps the previous call's contents and nothing in it needs to start at zero.
+ * Calls that overlap on one GPU (two streams, two threads, or a replayed
+ * graph and another call) share the array and race: serialise them. */
+int mi_moe_run_noalloc(const mi_moe_args* args, void* stream);
+
 /* Message of the last error on the calling thread ("" if none). */
 const char* mi_moe_last_error(void);
 

@@ -238,5 +238,20 @@ def test_header_constants_match_bindings():
     hdr = open(os.path.join(os.path.dirname(__file__), "..", "include", "mi_moe.h")).read()
     defs = dict(re.findall(r"#define (MI_MOE_[A-Z0-9_]+) (\d+)", hdr))
     for name in ("MI_MOE_OK", "MI_MOE_ERR_INVALID", "MI_MOE_ERR_WORKSPACE", "MI_MOE_ERR_HIP",
-                 "MI_MOE_DTYPE_BF16", "MI_MOE_DTYPE_F32", "MI_MOE_MAX_TOKENS"):
+                 "MI_MOE_DTYPE_BF16", "MI_MOE_DTYPE_F32", "MI_MOE_MAX_TOKENS",
+                 "MI_MOE_NOALLOC_MAX_TOKENS"):
         assert int(defs[name]) == getattr(_lib, name), name
+
+
+@cpu_only
+def test_run_noalloc_rejects_before_launch():
+    """The no-allocation entry point refuses a caller workspace and T above its
+    static scratch before looking anything up on a device."""
+    L = _lib.lib()
+    assert L.mi_moe_run_noalloc(None, None) == _lib.MI_MOE_ERR_INVALID
+    a = _args(workspace=1 << 30, workspace_bytes=0)
+    assert L.mi_moe_run_noalloc(ctypes.byref(a), None) == _lib.MI_MOE_ERR_INVALID
+    assert b"workspace must be NULL" in L.mi_moe_last_error()
+    a = _args(workspace=None, workspace_bytes=0, num_tokens=_lib.MI_MOE_NOALLOC_MAX_TOKENS + 1)
+    assert L.mi_moe_run_noalloc(ctypes.byref(a), None) == _lib.MI_MOE_ERR_INVALID
+    assert b"MI_MOE_NOALLOC_MAX_TOKENS" in L.mi_moe_last_error()
