@@ -1,25 +1,30 @@
 """Benchmark of the fused MoE on one MI355X.
 
-    python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload c1_t64]
-                    [--sweep | --no-sweep] [--no-cpu]
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload c3_t8192]
+                    [--sweep | --no-sweep] [--no-cpu] [--no-pmc]
 
 A step is one call of ``flashinfer_amd.kernel.run`` on the workload's
 synthetic inputs, already resident in HBM. The headline workload is the
-decode sweep's T=64 point (H=7168, I=2048, 32 local experts of 256, top-8,
-FP8 e4m3 block-scaled), which streams the active experts' weights and is
-bound by HBM bandwidth. W untimed calls, then 5 trials of K calls each,
-bracketed by ``torch.cuda.synchronize()``; ``value`` is the median trial's
+prefill point T=8192 (H=7168, I=2048, 32 local experts of 256, top-8, FP8
+e4m3 block-scaled; 11,559 local slots over 28 active experts), the largest
+of the metric's T = 1 / 256 / 8192, where the grouped GEMMs are bound by
+the matrix cores. W untimed calls, then 5 trials of K calls each, bracketed
+by ``torch.cuda.synchronize()``; ``value`` is the median trial's
 microseconds per call. A second pass of 5 x K calls records HIP events
-between the five kernels on the stream they run on, which gives each
-kernel's average duration. A third pass times single calls with the caches
-cold (a 512 MiB read before each call evicts the MALL and L2s), a fourth
-replays the call captured in a HIP graph, and the probes of libmi_peaks.so
-measure the HBM and MFMA rates this GPU achieves.
+between the kernels on the stream they run on, which gives each kernel's
+average duration. A third pass times single calls with the caches cold (a
+512 MiB read before each call evicts the MALL and L2s), a fourth replays the
+call captured in a HIP graph, and the probes of libmi_peaks.so measure the
+HBM and MFMA rates this GPU achieves.
 
 Rank 0 prints ONE JSON line. ``roofline`` covers the dominant kernel
-(GEMM1+SwiGLU at decode); ``call_roofline`` the whole call; ``sweep`` the
-other configurations; ``quantize_fp8`` the activation quantiser that
-feeds the operator; ``cpu_baseline`` the CPU oracle on this host.
+(GEMM1+SwiGLU; at T=8192 bound by FP8 MFMA), with HBM traffic and the MFMA
+busy fraction from rocprofv3 counter passes; ``kernels`` gives both GEMMs'
+rooflines; ``call_roofline`` the whole call; ``sweep`` the other
+configurations, each with its dominant kernel's roofline and, at the
+metric's points (T = 1 with and without a local slot, 256, 8192), the CPU
+oracle timed on this host (``cpu_baseline``); ``quantize_fp8`` the
+activation quantiser that feeds the operator.
 """
 from __future__ import annotations
 
@@ -52,8 +57,12 @@ PART_ROW_BYTES = H * 2                                                   # bf16 
 GEMM1_FLOPS_PER_SLOT = 2 * 2 * I * H
 GEMM2_FLOPS_PER_SLOT = 2 * H * I
 
-SWEEP = ["c1_t1", "c1_t4", "c1_t16", "c1_t64", "t256", "c2_t1024_o0", "c3_t8192",
+HEADLINE = "c3_t8192"
+SWEEP = ["c1_t1", "c1_t1_local", "c1_t4", "c1_t16", "c1_t64", "t256", "c2_t1024_o0", "c3_t8192",
          "c4_t14000_skew"]
+# The metric's points (T = 1 / 256 / 8192): each sweep entry of these carries
+# the CPU oracle timed on this host beside the GPU figures.
+METRIC_POINTS = ("c1_t1", "c1_t1_local", "t256", "c3_t8192")
 
 
 def log(msg):
@@ -70,6 +79,38 @@ def gemm1_bytes(S, A_e):
 
 def gemm2_bytes(S, A_e):
     return A_e * W2_EXPERT_BYTES + S * (ACT_ROW_BYTES + PART_ROW_BYTES)
+
+
+def kernel_rooflines(res):
+    """Roofline of each GEMM launch from its average duration (HIP events):
+    the binding bound is the larger of its algorithmic HBM bytes at 8 TB/s
+    and its flops at the matrix-core peak of the type it computes in (GEMM1
+    FP8, GEMM2 bf16); ``frac`` = that bound time / measured time."""
+    S, A_e = res["slots"], res["active_experts"]
+    out = {}
+    for name, nbytes, flops, peak, dtype in (
+            ("gemm1_swiglu", gemm1_bytes(S, A_e), S * GEMM1_FLOPS_PER_SLOT, FP8_PEAK_TFLOPS, "fp8"),
+            ("gemm2", gemm2_bytes(S, A_e), S * GEMM2_FLOPS_PER_SLOT, BF16_PEAK_TFLOPS, "bf16")):
+        us = res["phase_us"][name]
+        if S == 0 or us <= 0:
+            out[name] = {"bound": "latency", "note": "no local slot: nothing to stream or multiply",
+                         "avg_launch_us": us}
+            continue
+        t = us * 1e-6
+        t_hbm = nbytes / (HBM_PEAK_GBS * 1e9)
+        t_mfma = flops / (peak * 1e12)
+        if t_mfma >= t_hbm:
+            r = {"bound": "mfma", "achieved": round(flops / t / 1e12, 1), "peak": peak,
+                 "unit": "TFLOP/s", "mfma_dtype": dtype}
+        else:
+            r = {"bound": "hbm", "achieved": round(nbytes / t / 1e9, 1), "peak": HBM_PEAK_GBS,
+                 "unit": "GB/s"}
+        r["frac"] = round(max(t_hbm, t_mfma) / t, 4)
+        r.update({"avg_launch_us": round(us, 2), "algorithmic_bytes_per_launch": nbytes,
+                  "algorithmic_flops_per_launch": flops,
+                  "gbps": round(nbytes / t / 1e9, 1), "tflops": round(flops / t / 1e12, 1)})
+        out[name] = r
+    return out
 
 
 def make(name):
@@ -167,6 +208,10 @@ def time_workload(wl, steps, warmup, trials=5):
     res["gemm1_tflops"] = round(F1 / g1 / 1e12, 2) if g1 > 0 else None
     res["gemm2_gbps"] = round(gemm2_bytes(S, A_e) / g2 / 1e9, 1) if g2 > 0 else None
     res["gemm2_tflops"] = round(F2 / g2 / 1e12, 2) if g2 > 0 else None
+    res["kernels"] = kernel_rooflines(res)
+    # the dominant kernel: the GEMM launch that takes longest
+    dom = max(res["kernels"], key=lambda k: res["phase_us"][k])
+    res["roofline"] = dict(res["kernels"][dom], kernel=dom)
     del args, out
     return res
 
@@ -351,62 +396,95 @@ def profiler_inherited(env=None) -> bool:
     return any(k in preload for k in ("rocprof", "roctracer", "rocprofiler"))
 
 
-def pmc_traffic(workload, kernel_key, copy_mib=1024, timeout=180):
-    """HBM bytes per launch of the first kernel whose name contains
-    ``kernel_key``, from two rocprofv3 counter passes (FETCH_SIZE, then
-    WRITE_SIZE) over a short child run of this bench. Each pass also times a
-    device copy of ``copy_mib`` MiB, whose counter reading gives the scale
-    from counter units to bytes. Returns None, starting nothing, if rocprofv3
-    is unavailable or this process itself runs under a profiler; None if a
-    pass fails. Must run before this process touches the GPU."""
-    if profiler_inherited():
-        log("[bench] running under a profiler: counter passes skipped (traffic = null)")
-        return None
+def _pmc_pass(counters, workload, copy_mib, timeout):
+    """One rocprofv3 counter pass over a short child run of this bench on
+    ``workload`` (which also copies ``copy_mib`` MiB device-to-device first).
+    Returns {counter: {kernel name: [per-dispatch values]}}, or None."""
     exe = shutil.which("rocprofv3")
     if exe is None:
         return None
-    out = {"kernel_key": kernel_key, "copy_bytes": copy_mib << 20}
     env = dict(os.environ, TMPDIR="/tmp")
+    with tempfile.TemporaryDirectory(dir="/tmp") as d:
+        cmd = ["timeout", "-s", "KILL", str(timeout), exe, "--pmc", *counters, "--output-format",
+               "csv", "-d", d, "-o", "pmc", "--", sys.executable, "-u",
+               os.path.abspath(__file__), "--workload", workload, "--steps", "2",
+               "--warmup", "1", "--no-sweep", "--no-cpu", "--no-pmc",
+               "--copy-calib-mib", str(copy_mib)]
+        log(f"[bench] counter pass {' '.join(counters)} ...")
+        r = subprocess.run(cmd, capture_output=True, text=True, env=env, cwd="/tmp")
+        files = glob.glob(os.path.join(d, "**", "*counter_collection.csv"), recursive=True)
+        if r.returncode != 0 or not files:
+            log(f"[bench] counter pass {' '.join(counters)} failed (rc={r.returncode})")
+            return None
+        vals = {c: {} for c in counters}
+        with open(files[0]) as f:
+            for row in csv.DictReader(f):
+                c = row["Counter_Name"]
+                if c in vals:
+                    vals[c].setdefault(row["Kernel_Name"], []).append(float(row["Counter_Value"]))
+        return vals
+
+
+def _pick(per_kernel, key):
+    """Median per-dispatch value over the kernels whose name contains key."""
+    xs = [v for name, vs in per_kernel.items() if key in name for v in vs]
+    return statistics.median(xs) if xs else None
+
+
+def pmc_counters(workload, kernel_key, copy_mib=1024, timeout=240):
+    """Counters of the first kernel whose name contains ``kernel_key``, from
+    three rocprofv3 passes over short child runs of this bench (each pass a
+    process of its own): HBM bytes per launch from FETCH_SIZE and WRITE_SIZE,
+    each scaled to bytes by what the same counter reads for a device copy of
+    ``copy_mib`` MiB timed in the same pass; and the MFMA busy fraction,
+    SQ_VALU_MFMA_BUSY_CYCLES per SIMD (1024 SIMDs) over GRBM_GUI_ACTIVE per
+    XCD (8 XCDs). Returns None, starting nothing, if rocprofv3 is
+    unavailable or this process itself runs under a profiler; fields of a
+    failed pass are null. Must run before this process touches the GPU."""
+    if profiler_inherited():
+        log("[bench] running under a profiler: counter passes skipped (traffic = null)")
+        return None
+    if shutil.which("rocprofv3") is None:
+        return None
+    out = {"kernel_key": kernel_key, "copy_bytes": copy_mib << 20}
     for counter in ("FETCH_SIZE", "WRITE_SIZE"):
-        with tempfile.TemporaryDirectory(dir="/tmp") as d:
-            cmd = ["timeout", "-s", "KILL", str(timeout), exe, "--pmc", counter, "--output-format",
-                   "csv", "-d", d, "-o", "pmc", "--", sys.executable, "-u",
-                   os.path.abspath(__file__), "--workload", workload, "--steps", "2",
-                   "--warmup", "1", "--no-sweep", "--no-cpu", "--no-pmc",
-                   "--copy-calib-mib", str(copy_mib)]
-            log(f"[bench] counter pass {counter} ...")
-            r = subprocess.run(cmd, capture_output=True, text=True, env=env, cwd="/tmp")
-            files = glob.glob(os.path.join(d, "**", "*counter_collection.csv"), recursive=True)
-            if r.returncode != 0 or not files:
-                log(f"[bench] counter pass {counter} failed (rc={r.returncode}); traffic = null")
-                return None
-            kern, copy = [], []
-            with open(files[0]) as f:
-                for row in csv.DictReader(f):
-                    if row["Counter_Name"] != counter:
-                        continue
-                    v = float(row["Counter_Value"])
-                    if kernel_key in row["Kernel_Name"]:
-                        kern.append(v)
-                    elif "copyBuffer" in row["Kernel_Name"]:
-                        copy.append(v)
-            if not kern or not copy:
-                return None
-            k_units = statistics.median(kern)
-            c_units = max(copy)  # the calibration copy is the largest copy dispatch
-            scale = (copy_mib << 20) / c_units if c_units > 0 else 0.0
-            key = "fetch" if counter == "FETCH_SIZE" else "write"
-            out[f"{key}_counter"] = k_units
-            out[f"{key}_copy_counter"] = c_units
-            out[f"{key}_bytes"] = k_units * scale
-    out["bytes"] = out["fetch_bytes"] + out["write_bytes"]
+        vals = _pmc_pass([counter], workload, copy_mib, timeout)
+        key = "fetch" if counter == "FETCH_SIZE" else "write"
+        k_units = _pick(vals[counter], kernel_key) if vals else None
+        c_units = max((v for name, vs in vals[counter].items() if "copyBuffer" in name
+                       for v in vs), default=None) if vals else None
+        if k_units is None or not c_units:
+            out[f"{key}_bytes"] = None
+            continue
+        scale = (copy_mib << 20) / c_units
+        out[f"{key}_counter"] = k_units
+        out[f"{key}_copy_counter"] = c_units
+        out[f"{key}_scale"] = round(scale, 4)
+        out[f"{key}_bytes"] = k_units * scale
+    fb, wb = out.get("fetch_bytes"), out.get("write_bytes")
+    out["bytes"] = fb + wb if fb is not None and wb is not None else None
+    vals = _pmc_pass(["SQ_VALU_MFMA_BUSY_CYCLES", "GRBM_GUI_ACTIVE"], workload, 0, timeout)
+    busy = _pick(vals["SQ_VALU_MFMA_BUSY_CYCLES"], kernel_key) if vals else None
+    gui = _pick(vals["GRBM_GUI_ACTIVE"], kernel_key) if vals else None
+    out["mfma_busy_cycles"] = busy
+    out["gui_active_cycles"] = gui
+    out["mfma_busy_frac"] = round((busy / 1024) / (gui / 8), 4) if busy and gui else None
     return out
 
 
-def cpu_baseline(wl, reps=3):
-    """The CPU oracle (fp32 torch) on this host: 1 warmup + reps timed calls."""
+def host_cores():
+    try:
+        return len(os.sched_getaffinity(0))
+    except AttributeError:
+        return os.cpu_count() or 1
+
+
+def cpu_baseline(wl, reps):
+    """The CPU oracle (fp32 torch) on this host's cores: 1 warmup + ``reps``
+    timed calls of the whole workload (the oracle dequantises only the active
+    experts' weights), median."""
     from oracle import ref_moe as R
-    torch.set_num_threads(os.cpu_count() or 1)
+    torch.set_num_threads(host_cores())
     cores = torch.get_num_threads()
     args = wl.args()
     R.moe_forward(*args)
@@ -415,32 +493,35 @@ def cpu_baseline(wl, reps=3):
         t0 = time.perf_counter()
         R.moe_forward(*args)
         ts.append(time.perf_counter() - t0)
-    # A definition-style reference dequantises every local expert's weights
-    # each call; timed separately (one pass over the 32 experts).
+    return {"value": round(statistics.median(ts) * 1e6, 1), "unit": "us/call", "cores": cores,
+            "kind": "port",
+            "sample": f"full {wl.name} call (T={wl.T}), fp32 torch oracle dequantising only the "
+                      f"active experts, 1 warmup + {reps} timed, median"}
+
+
+def dequant_all_experts_us(wl):
+    """One pass of the CPU oracle's dequantisation over all 32 local experts'
+    weights, as a definition-style reference does on every call."""
+    from oracle import ref_moe as R
     t = wl.tensors
     t0 = time.perf_counter()
     for e in range(t["gemm1_weights"].shape[0]):
         R.dequant_blocks(t["gemm1_weights"][e], t["gemm1_weights_scale"][e])
         R.dequant_blocks(t["gemm2_weights"][e], t["gemm2_weights_scale"][e])
-    dq_all = time.perf_counter() - t0
-    return {"value": round(statistics.median(ts) * 1e6, 1), "unit": "us/call", "cores": cores,
-            "kind": "port",
-            "sample": f"full {wl.name} call (T={wl.T}), fp32 torch oracle, dequantising only the "
-                      f"active experts, 1 warmup + {reps} timed, median",
-            "dequant_all_experts_us": round(dq_all * 1e6, 1)}
+    return round((time.perf_counter() - t0) * 1e6, 1)
 
 
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=100)
-    ap.add_argument("--warmup", type=int, default=3)
-    ap.add_argument("--workload", default="c1_t64")
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--workload", default=HEADLINE)
     ap.add_argument("--sweep", dest="sweep", action="store_true", default=True)
     ap.add_argument("--no-sweep", dest="sweep", action="store_false")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-pmc", action="store_true",
-                    help="skip the rocprofv3 FETCH_SIZE / WRITE_SIZE passes (traffic = null)")
+                    help="skip the rocprofv3 counter passes (traffic and MFMA busy = null)")
     ap.add_argument("--vendor-gemm-ref", action="store_true",
                     help="only time plain vendor-library GEMMs of the operator's shapes and "
                          "print them as one JSON line")
@@ -452,10 +533,14 @@ def main():
               "(local_expert_offset selects the shard) and has no multi-GPU path. "
               "Run with --gpus 1.", file=sys.stderr)
         sys.exit(2)
-    traffic = None
+    counters = None
     if not a.no_pmc and not a.vendor_gemm_ref:
-        # counter passes run as child processes before this one uses the GPU
-        traffic = pmc_traffic(a.workload, "gemm1_")
+        # counter passes run as child processes before this one uses the GPU;
+        # the dominant kernel at the headline is the LDS-tiled GEMM1 above
+        # T = 1536, the K-split or wide GEMM1 below
+        from flashinfer_amd import workloads as W
+        key = "gemm1_tile" if W.STANDARD[a.workload]["T"] > 1536 else "gemm1_"
+        counters = pmc_counters(a.workload, key)
     if not torch.cuda.is_available():
         print("bench.py needs a ROCm GPU", file=sys.stderr)
         sys.exit(2)
@@ -484,7 +569,7 @@ def main():
                 sweep.append(head)
                 continue
             w = make(name)
-            steps = a.steps if w.T <= 1024 else max(10, a.steps // 5)
+            steps = a.steps if w.T <= 1024 else max(10, a.steps // 2)
             r = time_workload(w, steps, a.warmup)
             log(f"[bench] {json.dumps(r)}")
             sweep.append(r)
@@ -496,34 +581,48 @@ def main():
     if a.copy_calib_mib == 0:  # not in the counter passes: their largest copy calibrates
         peaks = measured_peaks()
         log(f"[bench] measured peaks {peaks}")
-    read_gbs = peaks["hbm_read_gbs"] if peaks else None
+
     cpu = None
     if not a.no_cpu:
-        log("[bench] CPU oracle baseline ...")
-        cpu = cpu_baseline(wl)
-        log(f"[bench] cpu {cpu}")
+        # the CPU oracle at the headline and at every metric point of the sweep
+        # (1 timed call above T = 1024, 3 below), after all GPU timing
+        for r in ([head] + [r for r in sweep if r is not head and r["workload"] in METRIC_POINTS]):
+            w = make(r["workload"])
+            log(f"[bench] CPU oracle baseline {w.name} ...")
+            r["cpu_baseline"] = cpu_baseline(w, 1 if w.T > 1024 else 3)
+            log(f"[bench] cpu {w.name} {r['cpu_baseline']}")
+            if r is head:
+                r["cpu_baseline"]["dequant_all_experts_us"] = dequant_all_experts_us(w)
+            del w
+        cpu = head["cpu_baseline"]
 
-    g1_us = head["phase_us"]["gemm1_swiglu"]
-    g1_bytes = gemm1_bytes(head["slots"], head["active_experts"])
-    achieved = g1_bytes / (g1_us * 1e-6) / 1e9 if g1_us > 0 else 0.0
+    roof = dict(head["roofline"])
+    if counters:
+        roof["traffic"] = round(counters["bytes"]) if counters.get("bytes") else None
+        roof["mfma_busy_frac"] = counters.get("mfma_busy_frac")
+    else:
+        roof["traffic"] = None
+    if peaks and roof.get("bound") == "mfma":
+        meas = peaks["fp8_mfma_tflops"] if roof.get("mfma_dtype") == "fp8" else peaks["bf16_mfma_tflops"]
+        roof["measured_peak"] = meas
+        roof["frac_of_measured_peak"] = round(roof["achieved"] / meas, 4)
+    elif peaks and roof.get("bound") == "hbm":
+        roof["measured_peak"] = peaks["hbm_read_gbs"]
+        roof["frac_of_measured_peak"] = round(roof["achieved"] / peaks["hbm_read_gbs"], 4)
     line = {
         "metric": "fused-MoE µs/call + FP8 TFLOP/s & HBM GB/s vs roofline at T=1/256/8192",
         "value": head["us_per_call"], "unit": "us/call", "n_gpus": 1, "steps": a.steps,
         "warmup": a.warmup, "ms_per_step": round(head["us_per_call"] / 1000.0, 5),
-        "higher_is_better": False, "scaling": "weak", "vs_baseline": None, "dtype": "fp8_e4m3 (GEMM1) / bf16 (GEMM2), fp32 accumulate",
+        "higher_is_better": False, "scaling": "weak", "vs_baseline": None,
+        "dtype": "fp8_e4m3 (GEMM1) / bf16 (GEMM2), fp32 accumulate",
         "data": "synthetic (seeded N(0,1) fp8 weights/activations, U scales, N(0,0.1) bias)",
         "config": {"workload": f"{wl.name}: one fused-MoE layer call, T={wl.T} tokens", "T": wl.T,
                    "H": H, "I": I, "experts_global": E_GLOBAL, "experts_local": 32, "top_k": 8,
                    "local_expert_offset": wl.local_expert_offset,
                    "slots": head["slots"], "active_experts": head["active_experts"],
                    "parallelism": "single GPU (one EP shard)"},
-        "roofline": {"kernel": "gemm1_swiglu", "bound": "hbm", "achieved": round(achieved, 1),
-                     "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(achieved / HBM_PEAK_GBS, 4),
-                     "traffic": round(traffic["bytes"]) if traffic else None,
-                     "algorithmic_bytes_per_launch": g1_bytes, "avg_launch_us": round(g1_us, 2),
-                     "measured_read_gbs": read_gbs,
-                     "frac_of_measured_read": round(achieved / read_gbs, 4) if read_gbs else None},
+        "roofline": roof,
+        "kernels": head["kernels"],
         "measured_peaks": peaks,
         "call_roofline": {"gbps": head["gbps"], "hbm_frac": head["hbm_frac"],
                           "tflops": head["tflops"], "roofline_frac": head["roofline_frac"],
@@ -531,7 +630,7 @@ def main():
                           "us_per_call_cold": head["us_per_call_cold"],
                           "us_per_call_graph": head["us_per_call_graph"],
                           "phase_us": head["phase_us"]},
-        "traffic_detail": traffic,
+        "counters": counters,
         "cpu_baseline": cpu,
         "sweep": sweep,
         "quantize_fp8": quant,

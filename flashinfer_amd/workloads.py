@@ -99,6 +99,9 @@ def make_workload(name, T, seed, local_expert_offset=0, skew=False, H=H_DEF, I=I
 STANDARD = {
     "c0_t16": dict(T=16, seed=100, local_expert_offset=0),
     "c1_t1": dict(T=1, seed=101, local_expert_offset=0),
+    # one token with two local slots (experts 10 and 23): single-token decode
+    # that streams two experts' weights (seed 101 routes its token elsewhere)
+    "c1_t1_local": dict(T=1, seed=121, local_expert_offset=0),
     "c1_t4": dict(T=4, seed=102, local_expert_offset=0),
     "c1_t16": dict(T=16, seed=103, local_expert_offset=0),
     "c1_t64": dict(T=64, seed=104, local_expert_offset=0),

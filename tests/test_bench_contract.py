@@ -34,7 +34,7 @@ def test_algorithmic_constants():
 def test_counter_passes_never_start_under_a_profiler(monkeypatch):
     """Run under rocprofv3 (its tool library preloaded), bench.py must not
     start its own rocprofv3 children: the profiler has already initialised
-    the GPU in this process. pmc_traffic returns None without spawning."""
+    the GPU in this process. pmc_counters returns None without spawning."""
     started = []
     monkeypatch.setattr(bench.subprocess, "run", lambda *a, **k: started.append(a) or None)
     monkeypatch.setattr(bench.shutil, "which", lambda name: "/opt/rocm/bin/" + name)
@@ -46,7 +46,7 @@ def test_counter_passes_never_start_under_a_profiler(monkeypatch):
         for k, v in env.items():
             monkeypatch.setenv(k, v)
         assert bench.profiler_inherited()
-        assert bench.pmc_traffic("c3_t8192", "gemm1_tile") is None
+        assert bench.pmc_counters("c3_t8192", "gemm1_tile") is None
     assert started == []
     # an unrelated preload is not a profiler
     assert not bench.profiler_inherited({"LD_PRELOAD": "/usr/lib/libharness.so"})
