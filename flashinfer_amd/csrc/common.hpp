@@ -204,10 +204,13 @@ hipError_t launch_gemm2_wide(const Plan& p, const uint8_t* w2, const float* w2s,
 // (64 rows for GEMM1, 32 for GEMM2; weights through a per-wave register
 // ring, activations through LDS) for medium row counts, 16 GEMM1 streaming
 // with K split over 4 waves of a workgroup, 17 GEMM2 fused with the combine
-// with K split over its 4 waves. An id without a kernel of its own in one GEMM
+// with K split over its 4 waves, 18 the GEMM1 LDS tile of variant 3 with the MFMA
+// operands swapped (one scale factor per lane and tile) and the scale FMAs
+// software-pipelined behind later MFMAs (for GEMM2, the tile of variant 3).
+// An id without a kernel of its own in one GEMM
 // (9, 10 and 17 for GEMM1, 9 and 16 for GEMM2) runs that GEMM's default
 // stream shape.
-constexpr int NUM_VARIANTS = 18;
+constexpr int NUM_VARIANTS = 19;
 // GEMM2 variants that also perform the combine (decode sizes only): tiles
 // dealt to the 4 waves, or k-blocks split over them.
 constexpr int VARIANT_GEMM2_COMBINE = 10;

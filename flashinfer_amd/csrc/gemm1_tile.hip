@@ -198,9 +198,207 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm1_tile_kernel(
     }
 }
 
+// The same tile with the MFMA operands swapped and the MFMAs software-
+// pipelined against their scale FMAs (variant 18).
+//
+// Weight rows are the MFMA's A operand and gathered activation rows its B
+// operand, so lane l receives D[4g+v][l%16]: four output columns 4g..4g+3 of
+// one row (r = l%16) of a 16x16 tile. The per-(row, k-block) activation
+// scale and the per-(128 columns, k-block) weight scale then combine into a
+// single factor u per lane and tile: 8 products per k-block per lane instead
+// of 32, and the SwiGLU epilogue stores 4 adjacent bf16 (8 bytes) per lane.
+// The activation scales sit in LDS as [row group][r][m], so one 16-byte read
+// gives a lane the scales of its rows m*16 + r (m = 0..3).
+//
+// Inside a k-block the 32 MFMAs of a wave (8 column tiles x 4 row tiles) run
+// as one sequence; the four scale-and-accumulate FMAs of MFMA t issue after
+// MFMA t+2, so they execute while the matrix core works on later tiles
+// rather than waiting on the result just issued. The last two MFMAs' FMAs
+// carry into the next k-block. Weight fragments are read from LDS one column
+// tile ahead.
+template <int WM, int WN, int GM>
+__global__ __launch_bounds__(64 * WM * WN) void gemm1_tile_t_kernel(
+    Plan p, const uint8_t* __restrict__ hs, const float* __restrict__ hs_scale,
+    const uint8_t* __restrict__ w1, const float* __restrict__ w1s) {
+    using C = G1Tile<WM, WN>;
+    static_assert(WN * 64 * 2 == 2 * C::BG && C::BG == 64 * WN, "column tiling");
+    __shared__ __attribute__((aligned(1024))) uint8_t smem[2 * C::STAGE];
+
+    int e, row0, nrows, nt;
+    if (!tile_coords<C::NT, GM>(p.meta, META_MTILE1, C::BM, e, row0, nrows, nt)) return;
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int jb = nt * C::BG;
+
+    uint32_t a_off[C::A_LD], b_off[C::B_LD];
+#pragma unroll
+    for (int i = 0; i < C::A_LD; ++i) {
+        const int row = 8 * (wave * C::A_LD + i) + (lane >> 3);
+        const int c = (lane & 7) ^ swzq(row);
+        const int tok = p.sorted_tok[row0 + min(row, nrows - 1)];
+        a_off[i] = (uint32_t)tok * H + c * 16;
+    }
+#pragma unroll
+    for (int i = 0; i < C::B_LD; ++i) {
+        const int row = 8 * (wave * C::B_LD + i) + (lane >> 3);
+        const int c = (lane & 7) ^ swzq(row);
+        const int wrow = row < C::BG ? jb + row : I + jb + (row - C::BG);
+        b_off[i] = (uint32_t)((e * N1 + wrow) * H + c * 16);
+    }
+    // scale loader: wave w < WM copies the 64 scales of rows 64w.., lane l
+    // to LDS position 64w + l, which holds row 64w + (l % 4) * 16 + l / 4
+    uint32_t sa_off = 0;
+    if (wave < C::SA_WAVES) {
+        const int row = 64 * wave + (lane & 3) * 16 + (lane >> 2);
+        sa_off = (uint32_t)p.sorted_tok[row0 + min(row, nrows - 1)];
+    }
+
+    auto issue = [&](int stage, int kb) __attribute__((always_inline)) {
+        uint8_t* s = smem + stage * C::STAGE;
+#pragma unroll
+        for (int i = 0; i < C::A_LD; ++i)
+            if (8 * (wave * C::A_LD + i) < nrows)
+                g2l16(hs + a_off[i] + kb * BLK, s + (wave * C::A_LD + i) * 1024);
+#pragma unroll
+        for (int i = 0; i < C::B_LD; ++i)
+            g2l16(w1 + b_off[i] + kb * BLK, s + C::A_BYTES + (wave * C::B_LD + i) * 1024);
+        if (wave < C::SA_WAVES)
+            g2l4(hs_scale + (size_t)kb * p.T + sa_off, s + C::A_BYTES + C::B_BYTES + wave * 256);
+    };
+
+    const int wm = wave % WM, wn = wave / WM;
+    const int r = lane & 15, g = lane >> 4;
+    const float* sbg_p = w1s + ((size_t)e * N1B + jb / BLK) * HB;
+    const float* sbu_p = w1s + ((size_t)e * N1B + (I + jb) / BLK) * HB;
+
+    // acc[n][m]: column tile n (0..3 gate, 4..7 up) x row tile m
+    v4f acc[8][4];
+    const v4f zero = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int n = 0; n < 8; ++n)
+#pragma unroll
+        for (int m = 0; m < 4; ++m) acc[n][m] = zero;
+
+    issue(0, 0);
+    wait_vmem();
+    __syncthreads();
+
+    const bool active = wm * 64 < nrows;  // wave-uniform: rows past the expert only copy
+    // MFMA results of the last two tiles of the previous k-block and their
+    // scale factors, applied early in the next one
+    v4f carry0 = zero, carry1 = zero;
+    float cu0 = 0.f, cu1 = 0.f;
+
+#pragma unroll 1
+    for (int kb = 0; kb < HB; ++kb) {
+        const int cur = kb & 1;
+        const uint8_t* sA = smem + cur * C::STAGE;
+        const uint8_t* sB = sA + C::A_BYTES;
+        const float* sSA = reinterpret_cast<const float*>(sB + C::B_BYTES);
+
+        v8i a[4];
+        float4 s4 = {0.f, 0.f, 0.f, 0.f};
+        auto read_b = [&](int n) __attribute__((always_inline)) {
+            const int brow = (n < 4) ? (wn * 64 + n * 16 + r) : (C::BG + wn * 64 + (n - 4) * 16 + r);
+            const uint8_t* base = sB + brow * BLK;
+            const int sw = swzq(brow);
+            const v4i lo = lds16(base + ((g ^ sw) << 4));
+            const v4i hi = lds16(base + (((g + 4) ^ sw) << 4));
+            return (v8i){lo.x, lo.y, lo.z, lo.w, hi.x, hi.y, hi.z, hi.w};
+        };
+        v8i bcur = {0, 0, 0, 0, 0, 0, 0, 0};
+        if (active) {
+#pragma unroll
+            for (int m = 0; m < 4; ++m) {
+                const int row = wm * 64 + m * 16 + r;
+                const uint8_t* base = sA + row * BLK;
+                const int sw = swzq(row);
+                const v4i lo = lds16(base + ((g ^ sw) << 4));
+                const v4i hi = lds16(base + (((g + 4) ^ sw) << 4));
+                a[m] = (v8i){lo.x, lo.y, lo.z, lo.w, hi.x, hi.y, hi.z, hi.w};
+            }
+            s4 = *reinterpret_cast<const float4*>(sSA + wm * 64 + r * 4);
+            bcur = read_b(0);
+        }
+        // The copy of k-block kb+1 goes out after this wave's fragment reads.
+        if (kb + 1 < HB) issue(cur ^ 1, kb + 1);
+        if (!active) {
+            wait_vmem();
+            __syncthreads();
+            continue;
+        }
+        const float sbg = sbg_p[kb], sbu = sbu_p[kb];
+        const float sam[4] = {s4.x, s4.y, s4.z, s4.w};
+        float ug[4], uu[4];
+#pragma unroll
+        for (int m = 0; m < 4; ++m) { ug[m] = sam[m] * sbg; uu[m] = sam[m] * sbu; }
+
+        v4f pr[32];
+        v8i bnext = bcur;
+#pragma unroll
+        for (int t = 0; t < 32; ++t) {
+            const int n = t >> 2, m = t & 3;
+            if (m == 0 && n + 1 < 8) bnext = read_b(n + 1);
+            pr[t] = mfma_f8_16x16x128(bcur, a[m], zero);
+            if (m == 3) bcur = bnext;
+            if (t >= 2) {
+                const int tn = (t - 2) >> 2, tm = (t - 2) & 3;
+                const float u = tn < 4 ? ug[tm] : uu[tm];
+#pragma unroll
+                for (int v = 0; v < 4; ++v) acc[tn][tm][v] += pr[t - 2][v] * u;
+            } else if (t == 0) {
+#pragma unroll
+                for (int v = 0; v < 4; ++v) acc[7][2][v] += carry0[v] * cu0;
+            } else {
+#pragma unroll
+                for (int v = 0; v < 4; ++v) acc[7][3][v] += carry1[v] * cu1;
+            }
+            __builtin_amdgcn_sched_barrier(0);
+        }
+        carry0 = pr[30];
+        carry1 = pr[31];
+        cu0 = uu[2];
+        cu1 = uu[3];
+        wait_vmem();
+        __syncthreads();
+    }
+#pragma unroll
+    for (int v = 0; v < 4; ++v) {
+        acc[7][2][v] += carry0[v] * cu0;
+        acc[7][3][v] += carry1[v] * cu1;
+    }
+
+    if (!active) return;
+#pragma unroll
+    for (int m = 0; m < 4; ++m) {
+        const int row = wm * 64 + m * 16 + r;
+        if (row < nrows) {
+#pragma unroll
+            for (int n = 0; n < 4; ++n) {
+                uint32_t w[2];
+#pragma unroll
+                for (int h = 0; h < 2; ++h) {
+                    const float v0 = silu(acc[n + 4][m][2 * h]) * acc[n][m][2 * h];
+                    const float v1 = silu(acc[n + 4][m][2 * h + 1]) * acc[n][m][2 * h + 1];
+                    w[h] = (uint32_t)f2bf(v0) | ((uint32_t)f2bf(v1) << 16);
+                }
+                *reinterpret_cast<uint2*>(p.act + (size_t)(row0 + row) * I + jb + wn * 64 + n * 16 +
+                                          4 * g) = make_uint2(w[0], w[1]);
+            }
+        }
+    }
+}
+
 hipError_t launch_gemm1_tile(const Plan& p, const uint8_t* hs, const float* hs_scale,
                              const uint8_t* w1, const float* w1s, int variant, hipStream_t s) {
-    if (variant == 3) {
+    if (variant == 18) {
+        using C = G1Tile<4, 2>;
+        const int tiles = max_mtiles(p.T, C::BM) * C::NT;
+        hipLaunchKernelGGL((gemm1_tile_t_kernel<4, 2, 16>), dim3((tiles + 7) / 8 * 8),
+                           dim3(C::THREADS), 0, s, p, hs, hs_scale, w1, w1s);
+    } else if (variant == 3) {
         using C = G1Tile<4, 2>;
         const int tiles = max_mtiles(p.T, C::BM) * C::NT;
         dim3 grid((tiles + 7) / 8 * 8);

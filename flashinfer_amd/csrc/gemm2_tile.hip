@@ -187,7 +187,7 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm2_tile_kernel(Plan p,
 
 hipError_t launch_gemm2_tile(const Plan& p, const uint8_t* w2, const float* w2s, int variant,
                              hipStream_t s) {
-    if (variant == 3) {
+    if (variant == 3 || variant == 18) {
         using C = G2Tile<2, 4>;
         const int tiles = max_mtiles(p.T, C::BM) * C::NT;
         dim3 grid((tiles + 7) / 8 * 8);

@@ -42,6 +42,14 @@ __device__ __forceinline__ void wait_vmem() { asm volatile("s_waitcnt vmcnt(0)" 
 // bank groups (conflict-free for 32- and 64-bank LDS).
 __device__ __forceinline__ int swz8(int row) { return (row & 7) ^ ((row >> 3) & 1); }
 
+// Swizzle of a 128-byte row whose reads are also conflict-free when 32 lanes
+// (16 rows x two adjacent chunks) are serviced together: for the four rows
+// r, r+4, r+8, r+12 that share a bank group the values differ in their upper
+// two bits, so chunks c and c^1 of those rows land on 8 distinct positions;
+// 16 rows at one chunk still take 16 distinct bank groups. A copy of 8 rows
+// x 8 chunks still reads each row's 128 bytes whole.
+__device__ __forceinline__ int swzq(int row) { return (((row >> 2) & 3) << 1) | ((row >> 1) & 1); }
+
 // Same for a 256-byte row of 16 chunks.
 __device__ __forceinline__ int swz16(int row) { return row & 15; }
 
