@@ -1,5 +1,6 @@
 """ctypes binding of libmi_moe.so (the C ABI in include/mi_moe.h), and of
-the libraries built for other (H, I) shapes (``shapes.py``), one per shape.
+the libraries built for other layer definitions (``shapes.py``: hidden and
+intermediate size, local experts, routing parameters), one per definition.
 
 The library is loaded after ``import torch`` so that its ``libamdhip64.so.7``
 dependency binds to the HIP runtime torch already loaded (same SONAME):
@@ -18,8 +19,9 @@ import torch  # noqa: F401  (must precede the CDLL load, see module docstring)
 from . import shapes
 
 HERE = os.path.dirname(os.path.abspath(__file__))
-LIB_PATH = os.path.join(HERE, "libmi_moe.so")  # the default shape (H=7168, I=2048)
+LIB_PATH = os.path.join(HERE, "libmi_moe.so")  # the default definition
 DEFAULT_SHAPE = shapes.DEFAULT_SHAPE
+DEFAULT = shapes.DEFAULT
 
 MI_MOE_OK = 0
 MI_MOE_ERR_INVALID = 1
@@ -32,8 +34,8 @@ MI_MOE_NOALLOC_MAX_TOKENS = 256  # largest num_tokens of mi_moe_run_noalloc
 
 EXPORTED = ("mi_moe_workspace_size", "mi_moe_workspace_layout", "mi_moe_run",
             "mi_moe_run_profiled", "mi_moe_run_bf16", "mi_moe_run_noalloc", "mi_moe_route",
-            "mi_moe_sort", "mi_moe_quantize_fp8", "mi_moe_shape", "mi_moe_last_error",
-            "mi_moe_version")
+            "mi_moe_sort", "mi_moe_quantize_fp8", "mi_moe_shape", "mi_moe_get_definition",
+            "mi_moe_last_error", "mi_moe_version")
 NUM_PHASES = 5
 PHASES = ("route", "sort", "gemm1_swiglu", "gemm2", "combine")
 
@@ -57,6 +59,12 @@ class MiMoeArgs(ctypes.Structure):
         ("workspace", ctypes.c_void_p),
         ("workspace_bytes", ctypes.c_size_t),
     ]
+
+
+class MiMoeDefinition(ctypes.Structure):
+    _fields_ = [(n, ctypes.c_int32) for n in
+                ("hidden_size", "intermediate_size", "num_local_experts", "num_experts", "n_group",
+                 "topk_group", "top_k")]
 
 
 class MiMoeLayout(ctypes.Structure):
@@ -104,44 +112,86 @@ def _bind(L: ctypes.CDLL) -> None:
     L.mi_moe_version.restype = ctypes.c_char_p
     L.mi_moe_shape.argtypes = [ctypes.POINTER(ctypes.c_int32), ctypes.POINTER(ctypes.c_int32)]
     L.mi_moe_shape.restype = ctypes.c_int
+    L.mi_moe_get_definition.argtypes = [ctypes.POINTER(MiMoeDefinition)]
+    L.mi_moe_get_definition.restype = ctypes.c_int
 
 
-def lib_path(shape=DEFAULT_SHAPE) -> str:
-    shape = (int(shape[0]), int(shape[1]))
-    return LIB_PATH if shape == DEFAULT_SHAPE else os.path.join(HERE, shapes.lib_name(*shape))
+def lib_path(defn=DEFAULT) -> str:
+    d = shapes.as_definition(defn)
+    return os.path.join(HERE, shapes.lib_name_of(d))
+
+
+def built_definitions() -> list:
+    """Every definition whose library is present next to this file."""
+    return [d for d in shapes.DEFINITIONS if os.path.exists(lib_path(d))]
 
 
 def built_shapes() -> list:
-    """(H, I) of every library present next to this file."""
-    return [sh for sh in shapes.SHAPES if os.path.exists(lib_path(sh))]
+    """(H, I) of every library present with the default routing and 32 local experts."""
+    return [(d.H, d.I) for d in built_definitions() if d.default_routing]
 
 
-def lib(shape=DEFAULT_SHAPE) -> ctypes.CDLL:
-    """The library compiled for ``shape`` = (H, I), loaded once."""
-    shape = (int(shape[0]), int(shape[1]))
-    L = _libs.get(shape)
+_DEF_FOR: dict = {}
+
+
+def definition_for(H: int, I: int, EL: int, EG: int):
+    """The built definition with hidden size H, intermediate size I, EL local
+    and EG global experts (tensor shapes fix these; the routing parameters
+    follow from the definition). Looked up once per key: the call path of
+    ``run`` stats no files."""
+    key = (H, I, EL, EG)
+    d = _DEF_FOR.get(key)
+    if d is not None:
+        return d
+    found = [d for d in built_definitions() if (d.H, d.I, d.EL, d.EG) == key]
+    if len(found) == 1:
+        _DEF_FOR[key] = found[0]
+        return found[0]
+    if not found:
+        d = shapes.Definition(H, I, EL, EG)
+        hint = ("add it to DEFINITIONS in flashinfer_amd/shapes.py and rebuild"
+                if shapes.supported(H, I) else "supported shapes have H % 1024 == 0 and I % 256 == 0")
+        raise ValueError(f"no library for hidden size {H}, intermediate size {I}, {EL} local of "
+                         f"{EG} experts (built: {[x.name for x in built_definitions()]}); {hint}"
+                         if d not in shapes.DEFINITIONS else
+                         f"{lib_path(d)} is missing: build it with `python -m flashinfer_amd.build`")
+    raise ValueError(f"several built definitions match H={H}, I={I}, {EL} of {EG} experts: "
+                     f"{[x.name for x in found]}")
+
+
+def lib(defn=DEFAULT) -> ctypes.CDLL:
+    """The library compiled for ``defn`` (a shapes.Definition, or an (H, I)
+    pair meaning the default routing), loaded once."""
+    d = shapes.as_definition(defn)
+    L = _libs.get(d)
     if L is not None:
         return L
     with _lock:
-        if shape in _libs:
-            return _libs[shape]
-        path = lib_path(shape)
+        if d in _libs:
+            return _libs[d]
+        path = lib_path(d)
         if not os.path.exists(path):
-            if shape == DEFAULT_SHAPE:
+            if d == DEFAULT:
                 raise RuntimeError(
                     f"{path} is missing: build it with `python -m flashinfer_amd.build` "
                     "(hipcc, gfx950). There is no non-native fallback.")
-            hint = ("add it to SHAPES in flashinfer_amd/shapes.py and rebuild"
-                    if shapes.supported(*shape) else
+            if d in shapes.DEFINITIONS:
+                raise ValueError(f"{path} is missing: build it with `python -m flashinfer_amd.build`")
+            hint = ("add it to DEFINITIONS in flashinfer_amd/shapes.py and rebuild"
+                    if shapes.supported(d.H, d.I) else
                     "supported shapes have H % 1024 == 0 and I % 256 == 0")
-            raise ValueError(f"no library for hidden size {shape[0]} and intermediate size "
-                             f"{shape[1]} (built: {built_shapes()}); {hint}")
+            raise ValueError(f"no library for hidden size {d.H} and intermediate size {d.I} "
+                             f"(built: {built_shapes()}); {hint}")
         L = ctypes.CDLL(path)
         _bind(L)
-        h, i = ctypes.c_int32(), ctypes.c_int32()
-        if L.mi_moe_shape(ctypes.byref(h), ctypes.byref(i)) != MI_MOE_OK or (h.value, i.value) != shape:
-            raise RuntimeError(f"{path} reports shape ({h.value}, {i.value}), expected {shape}")
-        _libs[shape] = L
+        got = MiMoeDefinition()
+        if L.mi_moe_get_definition(ctypes.byref(got)) != MI_MOE_OK:
+            raise RuntimeError(f"{path}: mi_moe_get_definition failed")
+        have = shapes.Definition(got.hidden_size, got.intermediate_size, got.num_local_experts,
+                                 got.num_experts, got.n_group, got.topk_group, got.top_k)
+        if have != d:
+            raise RuntimeError(f"{path} reports {have}, expected {d}")
+        _libs[d] = L
         return L
 
 
@@ -152,12 +202,18 @@ def check(code: int, L: ctypes.CDLL | None = None) -> None:
         raise MiMoeError(code, msg)
 
 
-def workspace_size(num_tokens: int, shape=DEFAULT_SHAPE) -> int:
-    return int(lib(shape).mi_moe_workspace_size(int(num_tokens)))
+def workspace_size(num_tokens: int, defn=DEFAULT) -> int:
+    return int(lib(defn).mi_moe_workspace_size(int(num_tokens)))
 
 
-def workspace_layout(num_tokens: int, shape=DEFAULT_SHAPE) -> MiMoeLayout:
+def workspace_layout(num_tokens: int, defn=DEFAULT) -> MiMoeLayout:
     out = MiMoeLayout()
-    L = lib(shape)
+    L = lib(defn)
     check(L.mi_moe_workspace_layout(int(num_tokens), ctypes.byref(out)), L)
     return out
+
+
+def meta_stride(defn=DEFAULT) -> int:
+    """Int offset between the expert-offset table and each row-tile prefix
+    table at the start of the workspace's meta region."""
+    return 64 if shapes.as_definition(defn).EL < 64 else 128

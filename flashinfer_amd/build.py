@@ -1,7 +1,8 @@
 """Builds libmi_moe.so (all HIP kernels + the C ABI, for the default
-H=7168, I=2048), one libmi_moe_h<H>_i<I>.so per further shape in
-shapes.SHAPES, and libmi_peaks.so (achievable-peak probes used by bench.py),
-for gfx950 with hipcc.
+definition: H=7168, I=2048, 32 of 256 experts, 8 groups, top-4 groups,
+top-8), one libmi_moe_<tag>.so per further definition in
+shapes.DEFINITIONS, and libmi_peaks.so (achievable-peak probes used by
+bench.py), for gfx950 with hipcc.
 
 Usage: python -m flashinfer_amd.build [--jobs N] [--save-temps]
 The shared libraries land next to this file so they travel with the tree.
@@ -15,7 +16,7 @@ import subprocess
 import sys
 from concurrent.futures import ThreadPoolExecutor
 
-from .shapes import SHAPES, lib_name
+from .shapes import DEFINITIONS, lib_name_of
 
 HERE = os.path.dirname(os.path.abspath(__file__))
 CSRC = os.path.join(HERE, "csrc")
@@ -55,11 +56,11 @@ def hipcc() -> str:
     return path
 
 
-def _compile(src: str, extra, shape=None) -> str:
-    sub = os.path.join(BUILD, f"h{shape[0]}_i{shape[1]}" if shape else "common")
+def _compile(src: str, extra, defn=None) -> str:
+    sub = os.path.join(BUILD, defn.tag if defn else "common")
     os.makedirs(sub, exist_ok=True)
     obj = os.path.join(sub, src.replace(".hip", ".o"))
-    defs = [f"-DMI_MOE_HIDDEN={shape[0]}", f"-DMI_MOE_INTER={shape[1]}"] if shape else []
+    defs = defn.defines() if defn else []
     cmd = [hipcc(), *HIPCC_FLAGS, *SOURCE_FLAGS.get(src, []), *defs, *extra,
            "-I", os.path.join(HERE, "..", "include"),
            "-c", os.path.join(CSRC, src), "-o", obj]
@@ -86,13 +87,13 @@ def _link(objs, out):
 
 def build(jobs: int = 8, extra=()) -> str:
     os.makedirs(BUILD, exist_ok=True)
-    jobs_list = [(s, shape) for shape in SHAPES for s in SOURCES] + [(s, None) for s in PEAKS_SOURCES]
+    jobs_list = [(s, d) for d in DEFINITIONS for s in SOURCES] + [(s, None) for s in PEAKS_SOURCES]
     with ThreadPoolExecutor(max_workers=jobs) as ex:
         objs = list(ex.map(lambda j: _compile(j[0], list(extra), j[1]), jobs_list))
     n = len(SOURCES)
-    for k, shape in enumerate(SHAPES):
-        _link(objs[k * n:(k + 1) * n], os.path.join(HERE, lib_name(*shape)))
-    _link(objs[len(SHAPES) * n:], PEAKS_LIB)
+    for k, d in enumerate(DEFINITIONS):
+        _link(objs[k * n:(k + 1) * n], os.path.join(HERE, lib_name_of(d)))
+    _link(objs[len(DEFINITIONS) * n:], PEAKS_LIB)
     return LIB
 
 

@@ -49,14 +49,14 @@ constexpr size_t align_up(size_t x) { return (x + 255) & ~(size_t)255; }
 constexpr mi_moe_layout make_layout(int64_t T) {
     mi_moe_layout L{};
     const size_t t = (size_t)(T < 0 ? 0 : T);
-    const size_t s_max = 8 * t;
+    const size_t s_max = (size_t)TOPK * t;  // local slots: at most TOPK per token
     size_t o = 0;
-    L.topk_ids = o;   o = align_up(o + t * TOPK * 4);
-    L.topk_w = o;     o = align_up(o + t * TOPK * 4);
+    L.topk_ids = o;   o = align_up(o + t * TOPK_LD * 4);
+    L.topk_w = o;     o = align_up(o + t * TOPK_LD * 4);
     L.expert_off = o; o = align_up(o + META_INTS * 4);
     L.sorted_tok = o; o = align_up(o + s_max * 4);
     L.sorted_w = o;   o = align_up(o + s_max * 4);
-    L.tok_slot = o;   o = align_up(o + t * TOPK * 4);
+    L.tok_slot = o;   o = align_up(o + t * TOPK_LD * 4);
     L.chunk_cnt = o;  o = align_up(o + (size_t)sort_chunks((int)t) * EL * 4);
     L.act = o;        o = align_up(o + s_max * I * 2);
     L.part = o;       o = align_up(o + s_max * H * 2);
@@ -233,7 +233,9 @@ const char* mi_moe_last_error(void) { return g_last_error.c_str(); }
 #define MI_MOE_STR2(x) #x
 #define MI_MOE_STR(x) MI_MOE_STR2(x)
 const char* mi_moe_version(void) {
-    return "mi_moe 0.1.0 gfx950 h" MI_MOE_STR(MI_MOE_HIDDEN) " i" MI_MOE_STR(MI_MOE_INTER);
+    return "mi_moe 0.2.0 gfx950 h" MI_MOE_STR(MI_MOE_HIDDEN) " i" MI_MOE_STR(MI_MOE_INTER) " e" MI_MOE_STR(
+        MI_MOE_E_LOCAL) " g" MI_MOE_STR(MI_MOE_E_GLOBAL) " ng" MI_MOE_STR(MI_MOE_N_GROUP) " kg" MI_MOE_STR(
+        MI_MOE_TOPK_GROUP) " k" MI_MOE_STR(MI_MOE_TOP_K);
 }
 
 int mi_moe_route(const float* routing_logits, const void* routing_bias, int32_t bias_dtype,
@@ -251,13 +253,26 @@ int mi_moe_route(const float* routing_logits, const void* routing_bias, int32_t 
     if (!routing_logits || !routing_bias || !topk_ids || !topk_weights)
         return fail(MI_MOE_ERR_INVALID, "mi_moe_route: NULL pointer argument");
     if (!aligned(routing_logits, 16) || !aligned(routing_bias, bias_dtype ? 16 : 8) ||
-        !aligned(topk_ids, 16) || !aligned(topk_weights, 16))
+        !aligned(topk_ids, 4) || !aligned(topk_weights, 4))
         return fail(MI_MOE_ERR_INVALID, "mi_moe_route: misaligned pointer");
     hipError_t err = launch_route(routing_logits, routing_bias, bias_dtype == MI_MOE_DTYPE_F32,
                                   (int)num_tokens, routed_scaling_factor, topk_ids, topk_weights,
-                                  (hipStream_t)stream);
+                                  (hipStream_t)stream, /*packed=*/true);
     if (err != hipSuccess)
         return fail(MI_MOE_ERR_HIP, "mi_moe_route: launch failed: %s", hipGetErrorString(err));
+    return MI_MOE_OK;
+}
+
+int mi_moe_get_definition(mi_moe_definition* out) {
+    g_last_error.clear();
+    if (!out) return fail(MI_MOE_ERR_INVALID, "mi_moe_get_definition: out is NULL");
+    out->hidden_size = H;
+    out->intermediate_size = I;
+    out->num_local_experts = EL;
+    out->num_experts = EG;
+    out->n_group = NGROUP;
+    out->topk_group = KGROUP;
+    out->top_k = TOPK;
     return MI_MOE_OK;
 }
 
@@ -279,17 +294,26 @@ int mi_moe_sort(const int32_t* topk_ids, const float* topk_weights, int64_t num_
     if (num_tokens == 0) return MI_MOE_OK;
     if (!topk_ids || !topk_weights || !workspace)
         return fail(MI_MOE_ERR_INVALID, "mi_moe_sort: NULL pointer argument");
-    if (!aligned(topk_ids, 16) || !aligned(topk_weights, 16) || !aligned(workspace, 256))
+    const bool direct = TOPK == TOPK_LD;  // rows already in the workspace's stride
+    if (!aligned(topk_ids, direct ? 16 : 4) || !aligned(topk_weights, direct ? 16 : 4) ||
+        !aligned(workspace, 256))
         return fail(MI_MOE_ERR_INVALID, "mi_moe_sort: misaligned pointer");
     const mi_moe_layout L = make_layout(num_tokens);
     if (workspace_bytes < L.total)
         return fail(MI_MOE_ERR_WORKSPACE, "mi_moe_sort: workspace has %zu bytes, needs %zu",
                     workspace_bytes, L.total);
     Plan p = make_plan(workspace, L, num_tokens, local_expert_offset, 0.f);
-    p.topk_ids = const_cast<int*>(topk_ids);  // read only
-    p.topk_w = const_cast<float*>(topk_weights);
+    hipError_t err = hipSuccess;
+    if (direct) {
+        p.topk_ids = const_cast<int*>(topk_ids);  // read only
+        p.topk_w = const_cast<float*>(topk_weights);
+    } else {  // [T, TOPK] rows -> the workspace's TOPK_LD-wide rows
+        err = launch_repack_topk(topk_ids, topk_weights, (int)num_tokens, p.topk_ids, p.topk_w,
+                                 (hipStream_t)stream);
+    }
     const Variants var = pick_variants(num_tokens);
-    hipError_t err = launch_sort(p, gemm1_bm(var.g1), gemm2_bm(var.g2), (hipStream_t)stream);
+    if (err == hipSuccess)
+        err = launch_sort(p, gemm1_bm(var.g1), gemm2_bm(var.g2), (hipStream_t)stream);
     if (err != hipSuccess)
         return fail(MI_MOE_ERR_HIP, "mi_moe_sort: launch failed: %s", hipGetErrorString(err));
     return MI_MOE_OK;

@@ -19,8 +19,8 @@ namespace mimoe {
 __global__ __launch_bounds__(256) void combine_kernel(Plan p, uint16_t* __restrict__ out) {
     const int t = blockIdx.x;
     const int c = blockIdx.y * 1024 + threadIdx.x * 4;
-    const int4 s0 = reinterpret_cast<const int4*>(p.tok_slot + (size_t)t * TOPK)[0];
-    const int4 s1 = reinterpret_cast<const int4*>(p.tok_slot + (size_t)t * TOPK)[1];
+    const int4 s0 = reinterpret_cast<const int4*>(p.tok_slot + (size_t)t * TOPK_LD)[0];
+    const int4 s1 = reinterpret_cast<const int4*>(p.tok_slot + (size_t)t * TOPK_LD)[1];
     const int slot[8] = {s0.x, s0.y, s0.z, s0.w, s1.x, s1.y, s1.z, s1.w};
     uint2 v[8];
 #pragma unroll

@@ -7,28 +7,67 @@
 
 namespace mimoe {
 
-// Problem shape (solution/triton/kernel.py:615-625 hard-codes H=7168,
-// I=2048). H and I are compile-time constants of each library build
-// (-DMI_MOE_HIDDEN / -DMI_MOE_INTER); routing, the 32 local experts and the
-// 128-element scale blocks are fixed by the ds-routing definition family.
+// Definition of the layer (solution/triton/kernel.py:615-625 hard-codes
+// H=7168, I=2048, 256 experts in 8 groups, top-4 groups, top-8, 32 local
+// experts; its routing kernel takes them as constexpr parameters,
+// kernel.py:371-389). Each library build fixes them at compile time:
+// -DMI_MOE_HIDDEN / -DMI_MOE_INTER / -DMI_MOE_E_LOCAL / -DMI_MOE_E_GLOBAL /
+// -DMI_MOE_N_GROUP / -DMI_MOE_TOPK_GROUP / -DMI_MOE_TOP_K. The scale blocks
+// stay 128 elements.
 #ifndef MI_MOE_HIDDEN
 #define MI_MOE_HIDDEN 7168
 #endif
 #ifndef MI_MOE_INTER
 #define MI_MOE_INTER 2048
 #endif
+#ifndef MI_MOE_E_LOCAL
+#define MI_MOE_E_LOCAL 32
+#endif
+#ifndef MI_MOE_E_GLOBAL
+#define MI_MOE_E_GLOBAL 256
+#endif
+#ifndef MI_MOE_N_GROUP
+#define MI_MOE_N_GROUP 8
+#endif
+#ifndef MI_MOE_TOPK_GROUP
+#define MI_MOE_TOPK_GROUP 4
+#endif
+#ifndef MI_MOE_TOP_K
+#define MI_MOE_TOP_K 8
+#endif
 constexpr int H = MI_MOE_HIDDEN;  // hidden size
 constexpr int I = MI_MOE_INTER;   // intermediate size
 // combine: 1024-column chunks; GEMM1 K split over 4 waves of 2-deep rings:
 // 8 | H/128. GEMM2 rings at least 2 deep, tiles of 128 columns: 2 | I/128.
 static_assert(H % 1024 == 0 && I % 256 == 0, "supported shapes: H % 1024 == 0, I % 256 == 0");
-constexpr int N1 = 2 * I;      // GEMM1 output width (gate | up)
-constexpr int EG = 256;        // global experts
-constexpr int EL = 32;         // local experts per shard
-constexpr int TOPK = 8;
-constexpr int NGROUP = 8;
-constexpr int KGROUP = 4;
-constexpr int GSIZE = EG / NGROUP;  // 32
+constexpr int N1 = 2 * I;                // GEMM1 output width (gate | up)
+constexpr int EG = MI_MOE_E_GLOBAL;      // global experts
+constexpr int EL = MI_MOE_E_LOCAL;       // local experts per shard
+constexpr int TOPK = MI_MOE_TOP_K;       // experts per token
+constexpr int NGROUP = MI_MOE_N_GROUP;   // routing groups
+constexpr int KGROUP = MI_MOE_TOPK_GROUP;  // groups a token may pick from
+constexpr int GSIZE = EG / NGROUP;       // experts per group
+// Routing: one wave64 per token, lane l owns experts EPL*l .. EPL*l+EPL-1;
+// a group is LPG adjacent lanes, reduced by DPP exchanges within 16 lanes.
+constexpr int EPL = EG / 64;
+constexpr int LPG = GSIZE / (EPL > 0 ? EPL : 1);
+static_assert(EG % 64 == 0 && EG <= 256, "global experts: 64, 128, 192 or 256");
+static_assert(EG % NGROUP == 0 && GSIZE % EPL == 0, "groups of whole lanes");
+static_assert(LPG == 2 || LPG == 4 || LPG == 8 || LPG == 16, "2 to 16 lanes per routing group");
+static_assert(KGROUP >= 1 && KGROUP <= NGROUP, "topk_group within the groups");
+static_assert(TOPK >= 1 && TOPK <= 8 && TOPK <= KGROUP * GSIZE, "top-k of 1..8 from the kept groups");
+// Local experts: one lane (and one ballot bit plane) per expert.
+static_assert(EL == 16 || EL == 32 || EL == 64, "16, 32 or 64 local experts");
+// Row stride of the per-token top-k tables and slot lists in the workspace:
+// always 8, entries past TOPK are padding, so every kernel loads a token's
+// row as two 16-byte vectors.
+constexpr int TOPK_LD = 8;
+// Bit mask over the local experts.
+typedef __typeof__(EL > 32 ? 0ull : 0u) emask_t;
+__device__ __forceinline__ emask_t ebit(int l) { return (emask_t)1 << l; }
+__device__ __forceinline__ int epopc(emask_t m) {
+    if constexpr (EL > 32) return __popcll(m); else return __popc((uint32_t)m);
+}
 constexpr int BLK = 128;            // scale block
 constexpr int HB = H / BLK;         // k-blocks of GEMM1 (56 at H=7168)
 constexpr int IB = I / BLK;         // k-blocks of GEMM2 (16 at I=2048)
@@ -39,21 +78,22 @@ struct Plan {
     int T;
     int local_offset;          // clamped into int range by the host
     float rsf;
-    int* topk_ids;             // [T, 8]
-    float* topk_w;             // [T, 8]
-    int* meta;                 // expert_off[33] | mtile_off1[33] | mtile_off2[33]
-    int* sorted_tok;           // [8T]
-    float* sorted_w;           // [8T]
-    int* tok_slot;             // [T, 8]
-    int* chunk_cnt;            // [ceil(T/1024), 32] per-chunk expert totals (large-T sort)
-    uint16_t* act;             // bf16 [8T, I]
-    uint16_t* part;            // bf16 [8T, H]: routing weight x GEMM2 row of each slot
+    int* topk_ids;             // [T, TOPK_LD]
+    float* topk_w;             // [T, TOPK_LD]
+    int* meta;                 // expert_off[EL+1] | mtile_off1[EL+1] | mtile_off2[EL+1]
+    int* sorted_tok;           // [TOPK*T]
+    float* sorted_w;           // [TOPK*T]
+    int* tok_slot;             // [T, TOPK_LD]
+    int* chunk_cnt;            // [ceil(T/1024), EL] per-chunk expert totals (large-T sort)
+    uint16_t* act;             // bf16 [TOPK*T, I]
+    uint16_t* part;            // bf16 [TOPK*T, H]: routing weight x GEMM2 row of each slot
 };
 
+constexpr int META_STRIDE = EL < 64 ? 64 : 128;  // holds EL + 1 entries
 constexpr int META_EXPERT_OFF = 0;
-constexpr int META_MTILE1 = 64;
-constexpr int META_MTILE2 = 128;
-constexpr int META_INTS = 192;
+constexpr int META_MTILE1 = META_STRIDE;
+constexpr int META_MTILE2 = 2 * META_STRIDE;
+constexpr int META_INTS = 3 * META_STRIDE;
 
 typedef int v4i __attribute__((ext_vector_type(4)));
 typedef int v8i __attribute__((ext_vector_type(8)));
@@ -112,6 +152,40 @@ __device__ __forceinline__ v8i ld_frag(const uint8_t* p) {
     return r;
 }
 
+// A token's top-k row in a TOPK_LD-strided table (workspace or LDS, 16-byte
+// aligned): stored as two 16-byte vectors, entries past TOPK as id -1,
+// weight 0; loaded the same way, keeping the first TOPK.
+__device__ __forceinline__ void store_topk_row(int* ids_row, float* w_row, const int ids[TOPK],
+                                               const float w[TOPK]) {
+    int iv[TOPK_LD];
+    float wv[TOPK_LD];
+#pragma unroll
+    for (int k = 0; k < TOPK_LD; ++k) {
+        iv[k] = k < TOPK ? ids[k < TOPK ? k : 0] : -1;
+        wv[k] = k < TOPK ? w[k < TOPK ? k : 0] : 0.f;
+    }
+    reinterpret_cast<int4*>(ids_row)[0] = make_int4(iv[0], iv[1], iv[2], iv[3]);
+    reinterpret_cast<int4*>(ids_row)[1] = make_int4(iv[4], iv[5], iv[6], iv[7]);
+    reinterpret_cast<float4*>(w_row)[0] = make_float4(wv[0], wv[1], wv[2], wv[3]);
+    reinterpret_cast<float4*>(w_row)[1] = make_float4(wv[4], wv[5], wv[6], wv[7]);
+}
+
+__device__ __forceinline__ void load_topk_ids(const int* ids_row, int ids[TOPK]) {
+    const int4 i0 = reinterpret_cast<const int4*>(ids_row)[0];
+    const int4 i1 = reinterpret_cast<const int4*>(ids_row)[1];
+    const int iv[TOPK_LD] = {i0.x, i0.y, i0.z, i0.w, i1.x, i1.y, i1.z, i1.w};
+#pragma unroll
+    for (int k = 0; k < TOPK; ++k) ids[k] = iv[k];
+}
+
+__device__ __forceinline__ void load_topk_w(const float* w_row, float w[TOPK]) {
+    const float4 w0 = reinterpret_cast<const float4*>(w_row)[0];
+    const float4 w1 = reinterpret_cast<const float4*>(w_row)[1];
+    const float wv[TOPK_LD] = {w0.x, w0.y, w0.z, w0.w, w1.x, w1.y, w1.z, w1.w};
+#pragma unroll
+    for (int k = 0; k < TOPK; ++k) w[k] = wv[k];
+}
+
 // Locate the expert and first row of row tile `mt` (prefix table in meta).
 __device__ __forceinline__ bool find_tile(const int* meta, int mtile_base, int mt, int bm, int& e,
                                           int& row0, int& nrows) {
@@ -127,18 +201,24 @@ __device__ __forceinline__ bool find_tile(const int* meta, int mtile_base, int m
 }
 
 // Upper bound on the row tiles of all experts: sum_e ceil(c_e / bm) with
-// sum_e c_e <= 8T, c_e <= T and at most min(32, 8T) experts holding slots
-// (each adds under one tile of rounding).
+// sum_e c_e <= TOPK*T, c_e <= T and at most min(EL, TOPK*T) experts holding
+// slots (each adds under one tile of rounding).
 inline int max_mtiles(int T, int bm) {
-    const long long a = (8LL * T + bm - 1) / bm + (8LL * T < EL ? 8LL * T : EL);
+    const long long st = (long long)TOPK * T;
+    const long long a = (st + bm - 1) / bm + (st < EL ? st : EL);
     const long long b = (long long)EL * ((T + bm - 1) / bm);
     return (int)(a < b ? a : b);
 }
 
 // Host-side launchers (one per kernel family); return hipError_t of the launch.
+// packed: rows of TOPK entries (the public routing entry point), else the
+// workspace's TOPK_LD-wide rows.
 hipError_t launch_route(const float* logits, const void* bias, int bias_is_f32, int T, float rsf,
-                        int* topk_ids, float* topk_w, hipStream_t s);
+                        int* topk_ids, float* topk_w, hipStream_t s, bool packed = false);
 hipError_t launch_sort(const Plan& p, int bm1, int bm2, hipStream_t s);
+// [T, TOPK] top-k rows -> TOPK_LD-wide rows (padding: id -1, weight 0).
+hipError_t launch_repack_topk(const int* ids, const float* w, int T, int* out_ids, float* out_w,
+                              hipStream_t s);
 // Routing + sort in one single-workgroup launch (small T only).
 bool route_sort_supported(int T);
 // Tokens per chunk of the large-T sort (one 1024-thread workgroup each).

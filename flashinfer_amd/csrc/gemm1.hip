@@ -51,7 +51,7 @@ void gemm1_stream_kernel(Plan p, const uint8_t* __restrict__ hs, const float* __
     // partial sums of waves 1..KS-1 of a column group: [split-1][group][value][lane]
     __shared__ float red[KS > 1 ? KS - 1 : 1][NW][KS > 1 ? 8 * MT : 1][64];
     // top-k of every token, routed in this workgroup (FRONT_ROUTE, T <= 64)
-    constexpr int RT = FRONT == FRONT_ROUTE ? SMALL_T * TOPK : 4;
+    constexpr int RT = FRONT == FRONT_ROUTE ? SMALL_T * TOPK_LD : 4;
     __shared__ __attribute__((aligned(16))) int s_ids[RT];
     __shared__ __attribute__((aligned(16))) float s_w[RT];
 
@@ -71,12 +71,7 @@ void gemm1_stream_kernel(Plan p, const uint8_t* __restrict__ hs, const float* __
                 int ids[TOPK];
                 float w[TOPK];
                 route_token(fa.logits + (size_t)t * EG, fa.bias, fa.bias_is_f32, p.rsf, lane, ids, w);
-                if (lane == 0) {
-                    reinterpret_cast<int4*>(s_ids + t * TOPK)[0] = make_int4(ids[0], ids[1], ids[2], ids[3]);
-                    reinterpret_cast<int4*>(s_ids + t * TOPK)[1] = make_int4(ids[4], ids[5], ids[6], ids[7]);
-                    reinterpret_cast<float4*>(s_w + t * TOPK)[0] = make_float4(w[0], w[1], w[2], w[3]);
-                    reinterpret_cast<float4*>(s_w + t * TOPK)[1] = make_float4(w[4], w[5], w[6], w[7]);
-                }
+                if (lane == 0) store_topk_row(s_ids + t * TOPK_LD, s_w + t * TOPK_LD, ids, w);
             }
             __syncthreads();
             ids_src = s_ids;
@@ -86,12 +81,12 @@ void gemm1_stream_kernel(Plan p, const uint8_t* __restrict__ hs, const float* __
         if (blockIdx.x == 0 && blockIdx.y == 0 && wave == 0) {
             if constexpr (FRONT == FRONT_ROUTE) {
                 if (lane < p.T) {  // the global top-k, as the routing kernel writes it
-                    int4* io = reinterpret_cast<int4*>(p.topk_ids + (size_t)lane * TOPK);
-                    float4* wo = reinterpret_cast<float4*>(p.topk_w + (size_t)lane * TOPK);
-                    io[0] = reinterpret_cast<const int4*>(s_ids + lane * TOPK)[0];
-                    io[1] = reinterpret_cast<const int4*>(s_ids + lane * TOPK)[1];
-                    wo[0] = reinterpret_cast<const float4*>(s_w + lane * TOPK)[0];
-                    wo[1] = reinterpret_cast<const float4*>(s_w + lane * TOPK)[1];
+                    int4* io = reinterpret_cast<int4*>(p.topk_ids + (size_t)lane * TOPK_LD);
+                    float4* wo = reinterpret_cast<float4*>(p.topk_w + (size_t)lane * TOPK_LD);
+                    io[0] = reinterpret_cast<const int4*>(s_ids + lane * TOPK_LD)[0];
+                    io[1] = reinterpret_cast<const int4*>(s_ids + lane * TOPK_LD)[1];
+                    wo[0] = reinterpret_cast<const float4*>(s_w + lane * TOPK_LD)[0];
+                    wo[1] = reinterpret_cast<const float4*>(s_w + lane * TOPK_LD)[1];
                 }
             }
             sort_one_wave<1>(p, ids_src, w_src, fa.bm1, fa.bm2, lane);

@@ -73,20 +73,19 @@ __global__ __launch_bounds__(64 * WIDE_NW) void gemm1_wide_kernel(Plan p, const 
     if constexpr (SORT) {
         static_assert(WIDE_NW * 64 >= 256 && BM == 64, "4 chunks of 64 tokens, 64-row tiles");
         const int t = wave * 64 + lane;
-        uint32_t m = 0;
+        emask_t m = 0;
         if (t < p.T) {
-            const int4 i0 = reinterpret_cast<const int4*>(p.topk_ids + (size_t)t * TOPK)[0];
-            const int4 i1 = reinterpret_cast<const int4*>(p.topk_ids + (size_t)t * TOPK)[1];
-            const int ids[TOPK] = {i0.x, i0.y, i0.z, i0.w, i1.x, i1.y, i1.z, i1.w};
+            int ids[TOPK];
+            load_topk_ids(p.topk_ids + (size_t)t * TOPK_LD, ids);
 #pragma unroll
             for (int k = 0; k < TOPK; ++k) {
                 const int l = ids[k] - p.local_offset;
-                m |= (unsigned)l < (unsigned)EL ? (1u << l) : 0u;
+                m |= (unsigned)l < (unsigned)EL ? ebit(l) : (emask_t)0;
             }
         }
 #pragma unroll
         for (int x = 0; x < EL; ++x) {
-            const unsigned long long bal = __ballot((m >> x) & 1u);
+            const unsigned long long bal = __ballot((m >> x) & 1);
             if (lane == x) s_bal[wave][x] = bal;
         }
         __syncthreads();

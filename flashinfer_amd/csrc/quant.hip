@@ -97,14 +97,7 @@ __global__ __launch_bounds__(256) void quant_route_kernel(
     int ids[TOPK];
     float w[TOPK];
     route_token(logits + (size_t)t * EG, bias, bias_is_f32, rsf, lane, ids, w);
-    if (lane == 0) {
-        int4* io = reinterpret_cast<int4*>(topk_ids + (size_t)t * TOPK);
-        float4* wo = reinterpret_cast<float4*>(topk_w + (size_t)t * TOPK);
-        io[0] = make_int4(ids[0], ids[1], ids[2], ids[3]);
-        io[1] = make_int4(ids[4], ids[5], ids[6], ids[7]);
-        wo[0] = make_float4(w[0], w[1], w[2], w[3]);
-        wo[1] = make_float4(w[4], w[5], w[6], w[7]);
-    }
+    if (lane == 0) store_topk_row(topk_ids + (size_t)t * TOPK_LD, topk_w + (size_t)t * TOPK_LD, ids, w);
 }
 
 hipError_t launch_quant_fp8(const void* x, int T, uint8_t* q, float* scale, hipStream_t s) {

@@ -1,19 +1,22 @@
 // DeepSeek no-aux routing of one token by one wavefront (device code shared
 // by the routing kernel and the fused routing + sort kernel).
 //
-// Follows solution/triton/kernel.py:371-457 (_route_select_local_kernel):
-//   s = sigmoid(logit), sb = s + bias                        (:400-404)
-//   group score = top1 + top2 of sb within each group of 32  (:406-416)
-//   keep the 4 best groups                                   (:418-426)
-//   pick the 8 best experts by sb inside them                (:428-438)
-//   w_k = s_k * rsf / (sum_k s_k + 1e-20)                    (:440, :450)
+// Follows solution/triton/kernel.py:371-457 (_route_select_local_kernel),
+// whose constexpr parameters E_GLOBAL, N_GROUP, TOPK_GROUP, TOP_K
+// (kernel.py:371-389) are this build's EG, NGROUP, KGROUP, TOPK:
+//   s = sigmoid(logit), sb = s + bias                               (:400-404)
+//   group score = top1 + top2 of sb within each group of EG/NGROUP   (:406-416)
+//   keep the KGROUP best groups                                      (:418-426)
+//   pick the TOPK best experts by sb inside them                     (:428-438)
+//   w_k = s_k * rsf / (sum_k s_k + 1e-20)                            (:440, :450)
 // Ties resolve to the lowest index, like tl.argmax.
 //
-// Lane l of the wave owns experts 4l..4l+3, so one routing group is 8 lanes.
-// Reductions use DPP lane exchanges (a few cycles each) and readlane, not
-// LDS permutes: the group top-2 is three DPP merges, and each of the 8
-// top-k rounds is one 4-step DPP max, 4 readlanes and a ballot for the
-// lowest index. No LDS, no barriers, one 1 KB coalesced load per token.
+// Lane l of the wave owns experts EPL*l .. EPL*l+EPL-1 (EPL = EG/64), so one
+// routing group is LPG adjacent lanes. Reductions use DPP lane exchanges (a
+// few cycles each) and readlane, not LDS permutes: the group top-2 is up to
+// four DPP merges, and each of the TOPK top-k rounds is one 4-step DPP max,
+// 4 readlanes and a ballot for the lowest index. No LDS, no barriers, one
+// coalesced load of the token's logits row.
 #pragma once
 
 #include "common.hpp"
@@ -64,68 +67,102 @@ __device__ __forceinline__ uint32_t wave_max_u32(uint32_t k) {
     return max(max(r0, r1), max(r2, r3));
 }
 
-// Routes token row `logits_row` ([256] fp32). Every lane of the wave gets
-// the same ids (selection order) and weights.
+// Routes one token's logits row ([EG] fp32). Every lane of the wave gets the
+// same ids (selection order) and weights.
 __device__ __forceinline__ void route_token(const float* __restrict__ logits_row,
                                             const void* __restrict__ bias, int bias_is_f32,
                                             float rsf, int lane, int ids[TOPK], float wts[TOPK]) {
-    const float4 x = reinterpret_cast<const float4*>(logits_row)[lane];
-    float b0, b1, b2, b3;
-    if (bias_is_f32) {
-        const float4 bb = reinterpret_cast<const float4*>(bias)[lane];
-        b0 = bb.x; b1 = bb.y; b2 = bb.z; b3 = bb.w;
+    static_assert(EPL == 1 || EPL == 2 || EPL == 4, "64, 128 or 256 global experts");
+    float x[EPL], bb[EPL];
+    if constexpr (EPL == 4) {
+        const float4 v = reinterpret_cast<const float4*>(logits_row)[lane];
+        x[0] = v.x; x[1] = v.y; x[2] = v.z; x[3] = v.w;
+        if (bias_is_f32) {
+            const float4 b = reinterpret_cast<const float4*>(bias)[lane];
+            bb[0] = b.x; bb[1] = b.y; bb[2] = b.z; bb[3] = b.w;
+        } else {
+            const uint2 raw = reinterpret_cast<const uint2*>(bias)[lane];
+            bb[0] = bf2f(raw.x & 0xffffu); bb[1] = bf2f(raw.x >> 16);
+            bb[2] = bf2f(raw.y & 0xffffu); bb[3] = bf2f(raw.y >> 16);
+        }
+    } else if constexpr (EPL == 2) {
+        const float2 v = reinterpret_cast<const float2*>(logits_row)[lane];
+        x[0] = v.x; x[1] = v.y;
+        if (bias_is_f32) {
+            const float2 b = reinterpret_cast<const float2*>(bias)[lane];
+            bb[0] = b.x; bb[1] = b.y;
+        } else {
+            const uint32_t raw = reinterpret_cast<const uint32_t*>(bias)[lane];
+            bb[0] = bf2f(raw & 0xffffu); bb[1] = bf2f(raw >> 16);
+        }
     } else {
-        const uint2 raw = reinterpret_cast<const uint2*>(bias)[lane];
-        b0 = bf2f(raw.x & 0xffffu); b1 = bf2f(raw.x >> 16);
-        b2 = bf2f(raw.y & 0xffffu); b3 = bf2f(raw.y >> 16);
+        x[0] = logits_row[lane];
+        bb[0] = bias_is_f32 ? reinterpret_cast<const float*>(bias)[lane]
+                            : bf2f(reinterpret_cast<const uint16_t*>(bias)[lane]);
     }
-    const float s[4] = {sigmoid_f32(x.x), sigmoid_f32(x.y), sigmoid_f32(x.z), sigmoid_f32(x.w)};
-    const float sb[4] = {s[0] + b0, s[1] + b1, s[2] + b2, s[3] + b3};
-
-    // Top-2 (as a multiset) of the lane's 4 values, then of the 8-lane group.
-    float m1 = fmaxf(sb[0], sb[1]), m2 = fminf(sb[0], sb[1]);
+    float s[EPL], sb[EPL];
 #pragma unroll
-    for (int j = 2; j < 4; ++j) {
-        const float v = sb[j];
-        if (v > m1) { m2 = m1; m1 = v; } else { m2 = fmaxf(m2, v); }
+    for (int j = 0; j < EPL; ++j) { s[j] = sigmoid_f32(x[j]); sb[j] = s[j] + bb[j]; }
+
+    // Top-2 (as a multiset) of the lane's values, then of the LPG-lane group.
+    float m1, m2;
+    if constexpr (EPL == 1) {
+        m1 = sb[0];
+        m2 = -__builtin_inff();
+    } else {
+        m1 = fmaxf(sb[0], sb[1]);
+        m2 = fminf(sb[0], sb[1]);
+#pragma unroll
+        for (int j = 2; j < EPL; ++j) {
+            const float v = sb[j];
+            if (v > m1) { m2 = m1; m1 = v; } else { m2 = fmaxf(m2, v); }
+        }
     }
     top2_merge(m1, m2, dpp_f<DPP_XOR1>(m1), dpp_f<DPP_XOR1>(m2));
-    top2_merge(m1, m2, dpp_f<DPP_XOR2>(m1), dpp_f<DPP_XOR2>(m2));
-    top2_merge(m1, m2, dpp_f<DPP_HALF_MIRROR>(m1), dpp_f<DPP_HALF_MIRROR>(m2));
-    const float gscore = m1 + m2;  // identical in the 8 lanes of the group
+    if constexpr (LPG >= 4) top2_merge(m1, m2, dpp_f<DPP_XOR2>(m1), dpp_f<DPP_XOR2>(m2));
+    if constexpr (LPG >= 8)
+        top2_merge(m1, m2, dpp_f<DPP_HALF_MIRROR>(m1), dpp_f<DPP_HALF_MIRROR>(m2));
+    if constexpr (LPG >= 16) top2_merge(m1, m2, dpp_f<DPP_MIRROR>(m1), dpp_f<DPP_MIRROR>(m2));
+    const float gscore = m1 + m2;  // identical in the LPG lanes of the group
 
-    // Rank of this lane's group among the 8 (lower index wins ties).
-    const int my_g = lane >> 3;
+    // Rank of this lane's group among the NGROUP (lower index wins ties).
+    const int my_g = lane / LPG;
     int rank = 0;
 #pragma unroll
     for (int h = 0; h < NGROUP; ++h) {
         const float gh = __builtin_bit_cast(
-            float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, gscore), h * 8));
+            float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, gscore), h * LPG));
         rank += (gh > gscore) || (gh == gscore && h < my_g);
     }
     const bool gsel = rank < KGROUP;
 
     // Candidate keys: order-preserving image of s+bias; 0 = not a candidate
     // (ord_f32 maps every non-NaN float, -inf included, above 0).
-    uint32_t key[4];
+    uint32_t key[EPL];
 #pragma unroll
-    for (int j = 0; j < 4; ++j) key[j] = gsel ? ord_f32(sb[j]) : 0u;
+    for (int j = 0; j < EPL; ++j) key[j] = gsel ? ord_f32(sb[j]) : 0u;
 
     float ss[TOPK];
 #pragma unroll
     for (int k = 0; k < TOPK; ++k) {
-        const uint32_t local = max(max(key[0], key[1]), max(key[2], key[3]));
+        uint32_t local = key[0];
+#pragma unroll
+        for (int j = 1; j < EPL; ++j) local = max(local, key[j]);
         const uint32_t best = wave_max_u32(local);
         // Lowest expert index holding the best key: lowest lane, then lowest j.
         const unsigned long long holders = __ballot(local == best);
         const int owner = __builtin_ctzll(holders);
-        const int jj = key[0] == best ? 0 : (key[1] == best ? 1 : (key[2] == best ? 2 : 3));
-        const int j_owner = __builtin_amdgcn_readlane(jj, owner);
-        const float sv = j_owner == 0 ? s[0] : (j_owner == 1 ? s[1] : (j_owner == 2 ? s[2] : s[3]));
-        ss[k] = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, sv), owner));
-        ids[k] = owner * 4 + j_owner;
+        int jj = EPL - 1;
 #pragma unroll
-        for (int j = 0; j < 4; ++j) key[j] = (lane == owner && j == j_owner) ? 0u : key[j];
+        for (int j = EPL - 2; j >= 0; --j) jj = key[j] == best ? j : jj;
+        const int j_owner = __builtin_amdgcn_readlane(jj, owner);
+        float sv = s[0];
+#pragma unroll
+        for (int j = 1; j < EPL; ++j) sv = j_owner == j ? s[j] : sv;
+        ss[k] = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, sv), owner));
+        ids[k] = owner * EPL + j_owner;
+#pragma unroll
+        for (int j = 0; j < EPL; ++j) key[j] = (lane == owner && j == j_owner) ? 0u : key[j];
     }
     float denom = ss[0];
 #pragma unroll

@@ -104,26 +104,16 @@ __global__ __launch_bounds__(1024) void route_sort_kernel(Plan p, const float* _
                                                           const void* __restrict__ bias,
                                                           int bias_is_f32, int bm1, int bm2) {
     __shared__ int wcnt[CHUNK / 64][EL];
-    __shared__ __attribute__((aligned(16))) int s_ids[ROUTE_SORT_MAX_T * TOPK];
-    __shared__ __attribute__((aligned(16))) float s_w[ROUTE_SORT_MAX_T * TOPK];
+    __shared__ __attribute__((aligned(16))) int s_ids[ROUTE_SORT_MAX_T * TOPK_LD];
+    __shared__ __attribute__((aligned(16))) float s_w[ROUTE_SORT_MAX_T * TOPK_LD];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     for (int t = wave; t < p.T; t += CHUNK / 64) {
         int ids[TOPK];
         float w[TOPK];
         route_token(logits + (size_t)t * EG, bias, bias_is_f32, p.rsf, lane, ids, w);
         if (lane == 0) {
-            const int4 i0 = make_int4(ids[0], ids[1], ids[2], ids[3]);
-            const int4 i1 = make_int4(ids[4], ids[5], ids[6], ids[7]);
-            const float4 w0 = make_float4(w[0], w[1], w[2], w[3]);
-            const float4 w1 = make_float4(w[4], w[5], w[6], w[7]);
-            reinterpret_cast<int4*>(p.topk_ids + (size_t)t * TOPK)[0] = i0;
-            reinterpret_cast<int4*>(p.topk_ids + (size_t)t * TOPK)[1] = i1;
-            reinterpret_cast<float4*>(p.topk_w + (size_t)t * TOPK)[0] = w0;
-            reinterpret_cast<float4*>(p.topk_w + (size_t)t * TOPK)[1] = w1;
-            reinterpret_cast<int4*>(s_ids + t * TOPK)[0] = i0;
-            reinterpret_cast<int4*>(s_ids + t * TOPK)[1] = i1;
-            reinterpret_cast<float4*>(s_w + t * TOPK)[0] = w0;
-            reinterpret_cast<float4*>(s_w + t * TOPK)[1] = w1;
+            store_topk_row(p.topk_ids + (size_t)t * TOPK_LD, p.topk_w + (size_t)t * TOPK_LD, ids, w);
+            store_topk_row(s_ids + t * TOPK_LD, s_w + t * TOPK_LD, ids, w);
         }
     }
     __syncthreads();
@@ -178,6 +168,30 @@ __global__ __launch_bounds__(1024) void sort_place_kernel(Plan p, int nchunks, i
 }
 
 bool route_sort_supported(int T) { return T > 0 && T <= ROUTE_SORT_MAX_T; }
+
+__global__ __launch_bounds__(256) void repack_topk_kernel(const int* __restrict__ ids,
+                                                          const float* __restrict__ w, int T,
+                                                          int* __restrict__ out_ids,
+                                                          float* __restrict__ out_w) {
+    const int t = blockIdx.x * 256 + threadIdx.x;
+    if (t >= T) return;
+    int iv[TOPK];
+    float wv[TOPK];
+#pragma unroll
+    for (int k = 0; k < TOPK; ++k) {
+        iv[k] = ids[(size_t)t * TOPK + k];
+        wv[k] = w[(size_t)t * TOPK + k];
+    }
+    store_topk_row(out_ids + (size_t)t * TOPK_LD, out_w + (size_t)t * TOPK_LD, iv, wv);
+}
+
+hipError_t launch_repack_topk(const int* ids, const float* w, int T, int* out_ids, float* out_w,
+                              hipStream_t s) {
+    if (T <= 0) return hipSuccess;
+    hipLaunchKernelGGL(repack_topk_kernel, dim3((T + 255) / 256), dim3(256), 0, s, ids, w, T,
+                       out_ids, out_w);
+    return hipGetLastError();
+}
 
 hipError_t launch_route_sort(const Plan& p, const float* logits, const void* bias, int bias_is_f32,
                              int bm1, int bm2, hipStream_t s) {

@@ -14,10 +14,10 @@ namespace mimoe {
 // Largest T the one-wave sort takes (lane t = token t).
 constexpr int SMALL_T = 64;
 
-// A token's local experts: bit mask over the 32 local ids, and per top-k
+// A token's local experts: bit mask over the EL local ids, and per top-k
 // position the local id (-1 if not local) and routing weight.
 struct TokLocal {
-    uint32_t m;
+    emask_t m;
     int lid[TOPK];
     float lw[TOPK];
 };
@@ -31,7 +31,7 @@ __device__ __forceinline__ TokLocal make_local(const int ids[TOPK], const float 
         const bool loc = (unsigned)l < (unsigned)EL;
         r.lid[k] = loc ? l : -1;
         r.lw[k] = ws[k];
-        r.m |= loc ? (1u << l) : 0u;
+        r.m |= loc ? ebit(l) : (emask_t)0;
     }
     return r;
 }
@@ -41,14 +41,8 @@ __device__ __forceinline__ TokLocal load_local(const int* ids_base, const float*
     int ids[TOPK];
     float ws[TOPK];
     if (valid) {
-        const int4 i0 = reinterpret_cast<const int4*>(ids_base + (size_t)t * TOPK)[0];
-        const int4 i1 = reinterpret_cast<const int4*>(ids_base + (size_t)t * TOPK)[1];
-        const float4 w0 = reinterpret_cast<const float4*>(w_base + (size_t)t * TOPK)[0];
-        const float4 w1 = reinterpret_cast<const float4*>(w_base + (size_t)t * TOPK)[1];
-        ids[0] = i0.x; ids[1] = i0.y; ids[2] = i0.z; ids[3] = i0.w;
-        ids[4] = i1.x; ids[5] = i1.y; ids[6] = i1.z; ids[7] = i1.w;
-        ws[0] = w0.x; ws[1] = w0.y; ws[2] = w0.z; ws[3] = w0.w;
-        ws[4] = w1.x; ws[5] = w1.y; ws[6] = w1.z; ws[7] = w1.w;
+        load_topk_ids(ids_base + (size_t)t * TOPK_LD, ids);
+        load_topk_w(w_base + (size_t)t * TOPK_LD, ws);
     } else {
 #pragma unroll
         for (int k = 0; k < TOPK; ++k) { ids[k] = -1 - EL; ws[k] = 0.f; }  // never local
@@ -56,7 +50,7 @@ __device__ __forceinline__ TokLocal load_local(const int* ids_base, const float*
     return make_local(ids, ws, valid ? off : 0);
 }
 
-// Exclusive prefix of the per-expert slot counts held by lanes 0..31 of the
+// Exclusive prefix of the per-expert slot counts held by lanes 0..EL-1 of the
 // calling wave (every lane of the wave must call). Optionally writes the
 // expert offsets and the row-tile prefixes for GEMM tiles of bm1 / bm2 rows.
 __device__ __forceinline__ int scan_counts(const Plan& p, int lane, int c, int bm1, int bm2,
@@ -132,7 +126,7 @@ __device__ inline void sort_one_wave(const Plan& p, const int* ids_base, const f
     int j = 0;
 #pragma unroll UNROLL
     for (int e = 0; e < EL; ++e) {
-        const bool hit = (tl.m >> e) & 1u;
+        const bool hit = (tl.m >> e) & 1;
         const unsigned long long bal = __ballot(hit);
         const int base = __builtin_amdgcn_readlane(off, e);
         if (hit) {
@@ -142,12 +136,12 @@ __device__ inline void sort_one_wave(const Plan& p, const int* ids_base, const f
             for (int k = 0; k < TOPK; ++k) w = (tl.lid[k] == e) ? tl.lw[k] : w;
             p.sorted_tok[pos] = lane;
             p.sorted_w[pos] = w;
-            p.tok_slot[(size_t)lane * TOPK + j] = pos;
+            p.tok_slot[(size_t)lane * TOPK_LD + j] = pos;
             ++j;
         }
     }
     if (valid)
-        for (; j < TOPK; ++j) p.tok_slot[(size_t)lane * TOPK + j] = -1;
+        for (; j < TOPK_LD; ++j) p.tok_slot[(size_t)lane * TOPK_LD + j] = -1;
 }
 
 // Writes the slots of one chunk given wcnt[wave][e] = first slot of expert e
@@ -163,7 +157,7 @@ __device__ __forceinline__ void place_with_prefix(const Plan& p, int t, bool val
     uint32_t bal_lo = 0, bal_hi = 0;
 #pragma unroll
     for (int e = 0; e < EL; ++e) {
-        const unsigned long long bal = __ballot((tl.m >> e) & 1u);
+        const unsigned long long bal = __ballot((tl.m >> e) & 1);
         if (lane == e) { bal_lo = (uint32_t)bal; bal_hi = (uint32_t)(bal >> 32); }
     }
     const int base_e = wcnt[wave][lane & (EL - 1)];
@@ -178,14 +172,14 @@ __device__ __forceinline__ void place_with_prefix(const Plan& p, int t, bool val
         const int base = __shfl(base_e, src);
         if (l >= 0) {
             const int pos = base + __popc(blo & lower_lo) + __popc(bhi & lower_hi);
-            const int j = __popc(tl.m & ((1u << l) - 1u));
+            const int j = epopc(tl.m & (ebit(l) - 1));
             p.sorted_tok[pos] = t;
             p.sorted_w[pos] = tl.lw[k];
-            p.tok_slot[(size_t)t * TOPK + j] = pos;
+            p.tok_slot[(size_t)t * TOPK_LD + j] = pos;
         }
     }
     if (valid)
-        for (int j = __popc(tl.m); j < TOPK; ++j) p.tok_slot[(size_t)t * TOPK + j] = -1;
+        for (int j = epopc(tl.m); j < TOPK_LD; ++j) p.tok_slot[(size_t)t * TOPK_LD + j] = -1;
 }
 
 // Position of the k-th set bit (k counted from 0) of a 64-bit mask; k must be
@@ -202,7 +196,7 @@ __device__ __forceinline__ int nth_set_bit(unsigned long long mask, int k) {
 }
 
 // Row tile `mt` of bm-row tiles in the slot order of sort_one_wave, found by
-// the calling wave from the top-k ids alone (ids_base: [T, 8], global or
+// the calling wave from the top-k ids alone (ids_base: [T, TOPK_LD], global or
 // LDS; T <= 64; every lane calls):
 // expert e, first slot row0 = expert_off[e] + rank0, rows, and the mask of
 // tokens (bit t = token t) that picked e. valid is false past the last tile.
@@ -214,24 +208,23 @@ struct WaveTile {
 
 __device__ __forceinline__ WaveTile wave_tile(const Plan& p, const int* ids_base, int lane, int mt,
                                               int bm) {
-    uint32_t m = 0;
+    emask_t m = 0;
     if (lane < p.T) {
-        const int4 i0 = reinterpret_cast<const int4*>(ids_base + (size_t)lane * TOPK)[0];
-        const int4 i1 = reinterpret_cast<const int4*>(ids_base + (size_t)lane * TOPK)[1];
-        const int ids[TOPK] = {i0.x, i0.y, i0.z, i0.w, i1.x, i1.y, i1.z, i1.w};
+        int ids[TOPK];
+        load_topk_ids(ids_base + (size_t)lane * TOPK_LD, ids);
 #pragma unroll
         for (int k = 0; k < TOPK; ++k) {
             const int l = ids[k] - p.local_offset;
-            m |= (unsigned)l < (unsigned)EL ? (1u << l) : 0u;
+            m |= (unsigned)l < (unsigned)EL ? ebit(l) : (emask_t)0;
         }
     }
     int cnt = 0;
 #pragma unroll
     for (int e = 0; e < EL; ++e) {
-        const unsigned long long bal = __ballot((m >> e) & 1u);
+        const unsigned long long bal = __ballot((m >> e) & 1);
         if (lane == e) cnt = __popcll(bal);
     }
-    // inclusive prefixes of slots and row tiles over lanes 0..31 (lane = expert)
+    // inclusive prefixes of slots and row tiles over lanes 0..EL-1 (lane = expert)
     const int tiles = (cnt + bm - 1) / bm;
     const int v0 = excl_prefix_small(cnt) + cnt;
     const int v1 = excl_prefix_small(tiles) + tiles;
@@ -249,7 +242,7 @@ __device__ __forceinline__ WaveTile wave_tile(const Plan& p, const int* ids_base
     w.rank0 = (mt - t0) * bm;
     w.row0 = s0 + w.rank0;
     w.nrows = min(bm, ce - w.rank0);
-    w.hits = __ballot((m >> ee) & 1u);
+    w.hits = __ballot((m >> ee) & 1);
     return w;
 }
 

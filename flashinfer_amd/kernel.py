@@ -24,8 +24,9 @@ import torch
 
 from . import _lib
 
-# Default shape (kernel.py:615-625); run() takes H and I from the weights and
-# uses the library built for them (flashinfer_amd/shapes.py).
+# Default definition (kernel.py:615-625); run() takes H, I, the local and the
+# global expert counts from the tensors and uses the library built for that
+# definition (flashinfer_amd/shapes.py), whose routing parameters it fixes.
 H, I, E_GLOBAL, E_LOCAL, BLOCK = 7168, 2048, 256, 32, 128
 FP8 = torch.float8_e4m3fn
 
@@ -74,14 +75,27 @@ def _workspace(device: torch.device, stream: int, nbytes: int) -> torch.Tensor:
     return ws
 
 
-def _shape_of(gemm1_weights) -> tuple:
-    """(H, I) from gemm1_weights [32, 2I, H]: the shape whose library runs the call."""
+_DEFN_BY_SHAPES: dict = {}
+
+
+def _definition_of(routing_logits, gemm1_weights):
+    """The definition whose library runs the call: H and I from gemm1_weights
+    [E, 2I, H], E local experts, G global experts from routing_logits [T, G]
+    (remembered per pair of shapes: the call path repeats no checks)."""
+    if isinstance(gemm1_weights, torch.Tensor) and isinstance(routing_logits, torch.Tensor):
+        d = _DEFN_BY_SHAPES.get((gemm1_weights.shape, routing_logits.shape[-1]))
+        if d is not None and routing_logits.dim() == 2:
+            return d
     if not isinstance(gemm1_weights, torch.Tensor) or gemm1_weights.dim() != 3:
-        raise ValueError("gemm1_weights must be a 3-D tensor [32, 2I, H]")
-    two_i, h = int(gemm1_weights.shape[1]), int(gemm1_weights.shape[2])
+        raise ValueError("gemm1_weights must be a 3-D tensor [E_local, 2I, H]")
+    if not isinstance(routing_logits, torch.Tensor) or routing_logits.dim() != 2:
+        raise ValueError("routing_logits must be a 2-D tensor [T, E_global]")
+    el, two_i, h = (int(x) for x in gemm1_weights.shape)
     if two_i % 2:
         raise ValueError(f"gemm1_weights: dimension 1 ({two_i}) must be 2I (even)")
-    return (h, two_i // 2)
+    d = _lib.definition_for(h, two_i // 2, el, int(routing_logits.shape[1]))
+    _DEFN_BY_SHAPES[(gemm1_weights.shape, routing_logits.shape[-1])] = d
+    return d
 
 
 def _expect(t: torch.Tensor, name: str, dtypes, shape) -> None:
@@ -96,16 +110,16 @@ def _expect(t: torch.Tensor, name: str, dtypes, shape) -> None:
 # The per-call host path matters at small T, where the GPU work of a call is
 # ~11 us: the raw HIP stream handle of the current stream, without building a
 # torch Stream object (torch's own accessor; None if this torch lacks it), and
-# workspace sizes cached per (T, shape).
+# workspace sizes cached per (T, definition).
 _RAW_STREAM = getattr(torch._C, "_cuda_getCurrentRawStream", None)
 _WS_SIZES: dict = {}
 
 
-def _ws_size(T: int, shape) -> int:
-    key = (T, shape)
+def _ws_size(T: int, defn) -> int:
+    key = (T, defn)
     n = _WS_SIZES.get(key)
     if n is None:
-        n = _WS_SIZES[key] = _lib.workspace_size(T, shape)
+        n = _WS_SIZES[key] = _lib.workspace_size(T, defn)
     return n
 
 
@@ -141,7 +155,7 @@ def _phase_timing_enabled() -> bool:
 
 
 def _emit_phase_timing(args, T: int) -> None:
-    shape = _shape_of(args[4])
+    defn = _definition_of(args[0], args[4])
     global _PHASE_TIMING_EMITTED
     device = args[-1].device
     with torch.cuda.device(device):
@@ -152,9 +166,9 @@ def _emit_phase_timing(args, T: int) -> None:
                   for i, name in enumerate(_lib.PHASES)}
         slots = 0
         if T > 0:
-            L = _lib.workspace_layout(T, shape)
-            meta = last_workspace(device)[L.expert_off:L.expert_off + (E_LOCAL + 1) * 4]
-            slots = int(meta.view(torch.int32)[E_LOCAL].item())
+            L = _lib.workspace_layout(T, defn)
+            meta = last_workspace(device)[L.expert_off:L.expert_off + (defn.EL + 1) * 4]
+            slots = int(meta.view(torch.int32)[defn.EL].item())
     phase_ms = {ref: sum(native[n] for n in names) for ref, names in _REFERENCE_PHASES}
     total = sum(phase_ms.values())
     payload = {"total_tokens": slots, "phase_ms": phase_ms, "total_ms": total,
@@ -205,22 +219,10 @@ def run_noalloc(routing_logits, routing_bias, hidden_states, hidden_states_scale
     serialised. No counterpart in the reference."""
     tensors = (routing_logits, routing_bias, hidden_states, hidden_states_scale, gemm1_weights,
                gemm1_weights_scale, gemm2_weights, gemm2_weights_scale, output)
-    if not isinstance(routing_logits, torch.Tensor) or routing_logits.dim() != 2:
-        raise ValueError("routing_logits must be a 2-D tensor [T, 256]")
-    T = int(routing_logits.shape[0])
-    shape = _shape_of(gemm1_weights)
-    H, I = shape
-    _expect(routing_logits, "routing_logits", (torch.float32,), (T, E_GLOBAL))
-    _expect(routing_bias, "routing_bias", (torch.bfloat16, torch.float32), (E_GLOBAL,))
-    _expect(hidden_states, "hidden_states", (FP8,), (T, H))
-    _expect(hidden_states_scale, "hidden_states_scale", (torch.float32,), (H // BLOCK, T))
-    _expect(gemm1_weights, "gemm1_weights", (FP8,), (E_LOCAL, 2 * I, H))
-    _expect(gemm1_weights_scale, "gemm1_weights_scale", (torch.float32,),
-            (E_LOCAL, 2 * I // BLOCK, H // BLOCK))
-    _expect(gemm2_weights, "gemm2_weights", (FP8,), (E_LOCAL, H, I))
-    _expect(gemm2_weights_scale, "gemm2_weights_scale", (torch.float32,),
-            (E_LOCAL, H // BLOCK, I // BLOCK))
-    _expect(output, "output", (torch.bfloat16,), (T, H))
+    T = int(routing_logits.shape[0]) if isinstance(routing_logits, torch.Tensor) else 0
+    defn = _definition_of(routing_logits, gemm1_weights)
+    _validate(defn, T, routing_logits, routing_bias, hidden_states, hidden_states_scale,
+              gemm1_weights, gemm1_weights_scale, gemm2_weights, gemm2_weights_scale, output)
     if T > _lib.MI_MOE_NOALLOC_MAX_TOKENS:
         raise ValueError(f"run_noalloc takes at most {_lib.MI_MOE_NOALLOC_MAX_TOKENS} tokens, "
                          f"got {T}; use run()")
@@ -236,7 +238,7 @@ def run_noalloc(routing_logits, routing_bias, hidden_states, hidden_states_scale
     rsf = _scalar(routed_scaling_factor, float)
     if T == 0:
         return None
-    L = _lib.lib(shape)
+    L = _lib.lib(defn)
     args = _lib.MiMoeArgs(
         routing_logits=routing_logits.data_ptr(), routing_bias=routing_bias.data_ptr(),
         hidden_states=hidden_states.data_ptr(), hidden_states_scale=hidden_states_scale.data_ptr(),
@@ -293,25 +295,32 @@ def run_bf16(routing_logits: torch.Tensor, routing_bias: torch.Tensor, hidden: t
     return hidden_states, hidden_states_scale
 
 
+def _validate(defn, T, routing_logits, routing_bias, hidden_states, hidden_states_scale,
+              gemm1_weights, gemm1_weights_scale, gemm2_weights, gemm2_weights_scale, output):
+    H, I, EL, EG = defn.H, defn.I, defn.EL, defn.EG
+    _expect(routing_logits, "routing_logits", (torch.float32,), (T, EG))
+    _expect(routing_bias, "routing_bias", (torch.bfloat16, torch.float32), (EG,))
+    _expect(hidden_states, "hidden_states", (FP8,), (T, H))
+    _expect(hidden_states_scale, "hidden_states_scale", (torch.float32,), (H // BLOCK, T))
+    _expect(gemm1_weights, "gemm1_weights", (FP8,), (EL, 2 * I, H))
+    _expect(gemm1_weights_scale, "gemm1_weights_scale", (torch.float32,),
+            (EL, 2 * I // BLOCK, H // BLOCK))
+    _expect(gemm2_weights, "gemm2_weights", (FP8,), (EL, H, I))
+    _expect(gemm2_weights_scale, "gemm2_weights_scale", (torch.float32,),
+            (EL, H // BLOCK, I // BLOCK))
+    _expect(output, "output", (torch.bfloat16,), (T, H))
+
+
 def _call(routing_logits, routing_bias, hidden_states, hidden_states_scale, gemm1_weights,
           gemm1_weights_scale, gemm2_weights, gemm2_weights_scale, local_expert_offset,
           routed_scaling_factor, output, events, hidden_bf16=None):
     if not isinstance(routing_logits, torch.Tensor) or routing_logits.dim() != 2:
-        raise ValueError("routing_logits must be a 2-D tensor [T, 256]")
+        raise ValueError("routing_logits must be a 2-D tensor [T, E_global]")
     T = int(routing_logits.shape[0])
-    shape = _shape_of(gemm1_weights)
-    H, I = shape
-    _expect(routing_logits, "routing_logits", (torch.float32,), (T, E_GLOBAL))
-    _expect(routing_bias, "routing_bias", (torch.bfloat16, torch.float32), (E_GLOBAL,))
-    _expect(hidden_states, "hidden_states", (FP8,), (T, H))
-    _expect(hidden_states_scale, "hidden_states_scale", (torch.float32,), (H // BLOCK, T))
-    _expect(gemm1_weights, "gemm1_weights", (FP8,), (E_LOCAL, 2 * I, H))
-    _expect(gemm1_weights_scale, "gemm1_weights_scale", (torch.float32,),
-            (E_LOCAL, 2 * I // BLOCK, H // BLOCK))
-    _expect(gemm2_weights, "gemm2_weights", (FP8,), (E_LOCAL, H, I))
-    _expect(gemm2_weights_scale, "gemm2_weights_scale", (torch.float32,),
-            (E_LOCAL, H // BLOCK, I // BLOCK))
-    _expect(output, "output", (torch.bfloat16,), (T, H))
+    defn = _definition_of(routing_logits, gemm1_weights)
+    H = defn.H
+    _validate(defn, T, routing_logits, routing_bias, hidden_states, hidden_states_scale,
+              gemm1_weights, gemm1_weights_scale, gemm2_weights, gemm2_weights_scale, output)
     tensors = (routing_logits, routing_bias, hidden_states, hidden_states_scale, gemm1_weights,
                gemm1_weights_scale, gemm2_weights, gemm2_weights_scale, output)
     if hidden_bf16 is not None:
@@ -335,22 +344,22 @@ def _call(routing_logits, routing_bias, hidden_states, hidden_states_scale, gemm
     if (events is None and _RAW_STREAM is not None
             and device.index == torch.cuda.current_device()):
         # hot path: no device switch and no torch Stream object
-        _issue(shape, T, device, _RAW_STREAM(device.index), None, ins, out, offset, rsf, None,
+        _issue(defn, T, device, _RAW_STREAM(device.index), None, ins, out, offset, rsf, None,
                hidden_bf16)
     else:
         with torch.cuda.device(device):
             cur = torch.cuda.current_stream(device)
-            _issue(shape, T, device, cur.cuda_stream, cur, ins, out, offset, rsf, events,
+            _issue(defn, T, device, cur.cuda_stream, cur, ins, out, offset, rsf, events,
                    hidden_bf16)
     if out is not output:
         with torch.no_grad():  # output may be a leaf that requires grad
             output.copy_(out)
 
 
-def _issue(shape, T, device, stream, cur, ins, out, offset, rsf, events, hidden_bf16):
+def _issue(defn, T, device, stream, cur, ins, out, offset, rsf, events, hidden_bf16):
     """Fills the argument block and calls the library on `stream`."""
-    L = _lib.lib(shape)
-    need = _ws_size(T, shape)
+    L = _lib.lib(defn)
+    need = _ws_size(T, defn)
     ws = _workspace(device, stream, need)
     args = _lib.MiMoeArgs(
         routing_logits=ins[0].data_ptr(), routing_bias=ins[1].data_ptr(),
@@ -379,58 +388,69 @@ def _issue(shape, T, device, stream, cur, ins, out, offset, rsf, events, hidden_
                                          arr, len(handles)), L)
 
 
-def route(routing_logits: torch.Tensor, routing_bias: torch.Tensor, routed_scaling_factor: float):
-    """Routing only: (global top-8 ids int32 [T,8] in selection order, weights fp32 [T,8])."""
+def route(routing_logits: torch.Tensor, routing_bias: torch.Tensor, routed_scaling_factor: float,
+          definition=None):
+    """Routing only: (global top-k ids int32 [T, k] in selection order,
+    weights fp32 [T, k]) under ``definition`` (a shapes.Definition; default:
+    moe_fp8_block_scale_ds_routing_topk8_ng8_kg4, 256 experts)."""
+    defn = _lib.DEFAULT if definition is None else definition
     T = int(routing_logits.shape[0])
-    _expect(routing_logits, "routing_logits", (torch.float32,), (T, E_GLOBAL))
-    _expect(routing_bias, "routing_bias", (torch.bfloat16, torch.float32), (E_GLOBAL,))
+    _expect(routing_logits, "routing_logits", (torch.float32,), (T, defn.EG))
+    _expect(routing_bias, "routing_bias", (torch.bfloat16, torch.float32), (defn.EG,))
     dev = routing_logits.device
-    ids = torch.empty(T, 8, dtype=torch.int32, device=dev)
-    w = torch.empty(T, 8, dtype=torch.float32, device=dev)
+    ids = torch.empty(T, defn.TOPK, dtype=torch.int32, device=dev)
+    w = torch.empty(T, defn.TOPK, dtype=torch.float32, device=dev)
     if T == 0:
         return ids, w
     lg = routing_logits.contiguous()
     bs = routing_bias.contiguous()
+    L = _lib.lib(defn)
     with torch.cuda.device(dev):
         stream = torch.cuda.current_stream(dev).cuda_stream
-        _lib.check(_lib.lib().mi_moe_route(
+        _lib.check(L.mi_moe_route(
             lg.data_ptr(), bs.data_ptr(),
             _lib.MI_MOE_DTYPE_BF16 if bs.dtype == torch.bfloat16 else _lib.MI_MOE_DTYPE_F32,
-            T, float(routed_scaling_factor), ids.data_ptr(), w.data_ptr(), ctypes.c_void_p(stream)))
+            T, float(routed_scaling_factor), ids.data_ptr(), w.data_ptr(), ctypes.c_void_p(stream)), L)
     return ids, w
 
 
-def sort(topk_ids: torch.Tensor, topk_weights: torch.Tensor, local_expert_offset: int):
+def sort(topk_ids: torch.Tensor, topk_weights: torch.Tensor, local_expert_offset: int,
+         definition=None):
     """Local-expert sort only (kernel.py:460-516), for staged checks: from global
-    top-8 ids int32 [T,8] and weights fp32 [T,8] (those of ``route``, or any
-    others), the tables ``run``'s sort builds. Returns ``(expert_offsets int32
-    [33], sorted_token_ids int32 [S], sorted_weights fp32 [S], token_slots int32
-    [T,8])``; slots are grouped by local expert, token-ascending inside one,
-    and a token's slots are listed by ascending local expert, then -1. Reading
-    S back synchronises the stream (a debugging entry point, not the hot path)."""
+    top-k ids int32 [T, k] and weights fp32 [T, k] (those of ``route``, or any
+    others), the tables ``run``'s sort builds under ``definition`` (default:
+    the default definition, k = 8, 32 local experts). Returns
+    ``(expert_offsets int32 [E+1], sorted_token_ids int32 [S], sorted_weights
+    fp32 [S], token_slots int32 [T, 8])``; slots are grouped by local expert,
+    token-ascending inside one, and a token's slots are listed by ascending
+    local expert, then -1. Reading S back synchronises the stream (a debugging
+    entry point, not the hot path)."""
+    defn = _lib.DEFAULT if definition is None else definition
     if not isinstance(topk_ids, torch.Tensor) or topk_ids.dim() != 2:
-        raise ValueError("topk_ids must be a 2-D tensor [T, 8]")
+        raise ValueError(f"topk_ids must be a 2-D tensor [T, {defn.TOPK}]")
     T = int(topk_ids.shape[0])
-    _expect(topk_ids, "topk_ids", (torch.int32,), (T, 8))
-    _expect(topk_weights, "topk_weights", (torch.float32,), (T, 8))
+    _expect(topk_ids, "topk_ids", (torch.int32,), (T, defn.TOPK))
+    _expect(topk_weights, "topk_weights", (torch.float32,), (T, defn.TOPK))
     dev = topk_ids.device
     if dev.type != "cuda" or topk_weights.device != dev:
         raise ValueError("sort() needs both tensors on the same ROCm GPU")
     offset = _scalar(local_expert_offset, int)
+    EL = defn.EL
     if T == 0:
         empty = torch.empty(0, dtype=torch.int32, device=dev)
-        return (torch.zeros(E_LOCAL + 1, dtype=torch.int32, device=dev), empty,
+        return (torch.zeros(EL + 1, dtype=torch.int32, device=dev), empty,
                 torch.empty(0, dtype=torch.float32, device=dev),
                 torch.empty(0, 8, dtype=torch.int32, device=dev))
     ids, w = topk_ids.contiguous(), topk_weights.contiguous()
+    Lib = _lib.lib(defn)
     with torch.cuda.device(dev):
         stream = torch.cuda.current_stream(dev).cuda_stream
-        ws = _workspace(dev, stream, _lib.workspace_size(T))
-        _lib.check(_lib.lib().mi_moe_sort(ids.data_ptr(), w.data_ptr(), T, offset, ws.data_ptr(),
-                                          ws.numel(), ctypes.c_void_p(stream)))
-        L = _lib.workspace_layout(T)
-        eoff = ws[L.expert_off:L.expert_off + (E_LOCAL + 1) * 4].view(torch.int32).clone()
-        S = int(eoff[E_LOCAL].item())
+        ws = _workspace(dev, stream, _lib.workspace_size(T, defn))
+        _lib.check(Lib.mi_moe_sort(ids.data_ptr(), w.data_ptr(), T, offset, ws.data_ptr(),
+                                   ws.numel(), ctypes.c_void_p(stream)), Lib)
+        L = _lib.workspace_layout(T, defn)
+        eoff = ws[L.expert_off:L.expert_off + (EL + 1) * 4].view(torch.int32).clone()
+        S = int(eoff[EL].item())
         stok = ws[L.sorted_tok:L.sorted_tok + S * 4].view(torch.int32).clone()
         sw = ws[L.sorted_w:L.sorted_w + S * 4].view(torch.float32).clone()
         slots = ws[L.tok_slot:L.tok_slot + T * 32].view(torch.int32).view(T, 8).clone()
@@ -449,9 +469,10 @@ def quantize_activations(hidden: torch.Tensor, hidden_states: torch.Tensor | Non
     if not isinstance(hidden, torch.Tensor) or hidden.dim() != 2:
         raise ValueError("hidden must be a 2-D tensor [T, H]")
     T, H = int(hidden.shape[0]), int(hidden.shape[1])
-    shape = next((sh for sh in _lib.built_shapes() if sh[0] == H), None)
-    if shape is None:
-        raise ValueError(f"no library for hidden size {H} (built: {_lib.built_shapes()})")
+    defn = next((d for d in _lib.built_definitions() if d.H == H), None)
+    if defn is None:
+        raise ValueError(f"no library for hidden size {H} "
+                         f"(built: {[d.name for d in _lib.built_definitions()]})")
     _expect(hidden, "hidden", (torch.bfloat16,), (T, H))
     dev = hidden.device
     if hidden_states is None:
@@ -472,7 +493,7 @@ def quantize_activations(hidden: torch.Tensor, hidden_states: torch.Tensor | Non
     x = hidden.contiguous()
     with torch.cuda.device(dev):
         stream = torch.cuda.current_stream(dev).cuda_stream
-        L = _lib.lib(shape)
+        L = _lib.lib(defn)
         _lib.check(L.mi_moe_quantize_fp8(
             x.data_ptr(), T, hidden_states.data_ptr(), hidden_states_scale.data_ptr(),
             ctypes.c_void_p(stream)), L)

@@ -39,6 +39,8 @@ class Workload:
     skew: bool = False
     routed_scaling_factor: float = 2.5
     tensors: dict = field(default_factory=dict)
+    # routing of the definition (n_group, topk_group, top_k), for the oracle
+    routing: tuple = (8, 4, 8)
 
     def args(self, device=None):
         """Positional arguments of ``run`` (minus ``output``) in reference order."""
@@ -88,11 +90,19 @@ def make_tokens(T, seed, H=H_DEF, E_global=E_GLOBAL_DEF, skew=False, local_exper
 
 def make_workload(name, T, seed, local_expert_offset=0, skew=False, H=H_DEF, I=I_DEF,
                   E_global=E_GLOBAL_DEF, E_local=E_LOCAL_DEF, weight_seed=WEIGHT_SEED,
-                  routed_scaling_factor=2.5) -> Workload:
+                  routed_scaling_factor=2.5, routing=(8, 4, 8)) -> Workload:
     tens = make_tokens(T, seed, H, E_global, skew, local_expert_offset)
     tens.update(make_weights(H, I, E_local, weight_seed))
     return Workload(name=name, T=T, seed=seed, local_expert_offset=local_expert_offset,
-                    skew=skew, routed_scaling_factor=routed_scaling_factor, tensors=tens)
+                    skew=skew, routed_scaling_factor=routed_scaling_factor, tensors=tens,
+                    routing=tuple(routing))
+
+
+def make_for(defn, name, T, seed, **kw) -> Workload:
+    """A workload for a shapes.Definition: its H, I, local and global expert
+    counts and routing parameters."""
+    return make_workload(name, T, seed, H=defn.H, I=defn.I, E_global=defn.EG, E_local=defn.EL,
+                         routing=(defn.NG, defn.KG, defn.TOPK), **kw)
 
 
 # The five workload families of the benchmark definition (T, offsets, skew).

@@ -6,9 +6,12 @@
  * moe_fp8_block_scale_ds_routing_topk8_ng8_kg4_e32_h7168_i2048
  * (H = 7168, I = 2048, 256 global experts in 8 groups of 32, top-4 groups,
  * top-8 experts, 128-element scale blocks). The shapes below are written for
- * that H and I; a library built for another (H, I) (mi_moe_shape) takes the
+ * that definition; a library built for another one (mi_moe_get_definition:
+ * hidden size H, intermediate size I, E local experts, G global experts in
+ * n_group groups, topk_group groups kept, top_k experts per token) takes the
  * same layouts with 7168 -> H, 2048 -> I, 4096 -> 2I, 56 -> H/128,
- * 32 (GEMM1 n-blocks) -> 2I/128 and 16 -> I/128.
+ * 32 (GEMM1 n-blocks) -> 2I/128, 16 -> I/128, 32 (experts) -> E, 256 -> G
+ * and 8 (top-k) -> top_k.
  *
  * All pointers are device pointers; the caller owns every buffer, including
  * the workspace. The library never allocates device memory, never
@@ -64,16 +67,20 @@ typedef struct mi_moe_args {
 } mi_moe_args;
 
 /* Byte offsets of the intermediate buffers inside the workspace, for staged
- * parity checks. Layout of each buffer:
+ * parity checks. Layout of each buffer (k = top_k, rows of the [T, 8] tables
+ * are 8 wide whatever k is; entries past k are padding):
  *   topk_ids   int32 [T, 8]   global expert ids in selection order
  *   topk_w     fp32  [T, 8]   routing weights (kernel.py:450)
- *   expert_off int32 [33]     exclusive prefix of local slot counts (S = [32])
- *   sorted_tok int32 [8T]     token of each slot, expert-major, token-ascending
- *   sorted_w   fp32  [8T]     routing weight of each slot
+ *   expert_off int32 [E+1]    exclusive prefix of local slot counts (S = [E]),
+ *                             followed by the row-tile prefixes of the default
+ *                             GEMM kernels at int offsets 64 and 128 (E <= 32)
+ *                             or 128 and 256 (E = 64)
+ *   sorted_tok int32 [kT]     token of each slot, expert-major, token-ascending
+ *   sorted_w   fp32  [kT]     routing weight of each slot
  *   tok_slot   int32 [T, 8]   slots of each token, ascending local expert, -1 pad
- *   chunk_cnt  int32 [ceil(T/1024), 32]  per-1024-token-chunk local expert counts
- *   act        bf16  [8T, 2048]  SwiGLU(GEMM1) per slot
- *   part       bf16  [8T, 7168]  routing weight x GEMM2 row per slot        */
+ *   chunk_cnt  int32 [ceil(T/1024), E]  per-1024-token-chunk local expert counts
+ *   act        bf16  [kT, 2048]  SwiGLU(GEMM1) per slot
+ *   part       bf16  [kT, 7168]  routing weight x GEMM2 row per slot        */
 typedef struct mi_moe_layout {
     size_t topk_ids, topk_w, expert_off, sorted_tok, sorted_w, tok_slot, chunk_cnt, act, part;
     size_t total;
@@ -113,21 +120,23 @@ int mi_moe_run_profiled(const mi_moe_args* args, void* stream, void* const* even
 int mi_moe_run_bf16(const mi_moe_args* args, const void* hidden_bf16, void* stream);
 
 /* Routing only (kernel.py:371-457 without the local filter): writes global
- * top-8 ids (int32 [T, 8], selection order) and weights (fp32 [T, 8]). */
+ * top-k ids (int32 [T, top_k], selection order) and weights (fp32
+ * [T, top_k]); 4-byte aligned. */
 int mi_moe_route(const float* routing_logits, const void* routing_bias, int32_t bias_dtype,
                  int64_t num_tokens, float routed_scaling_factor, int32_t* topk_ids,
                  float* topk_weights, void* stream);
 
 /* Local-expert sort only (kernel.py:460-516 and the scan at :572-581), for
- * staged parity: from global top-8 ids (int32 [T, 8]) and weights (fp32
- * [T, 8]), e.g. those of mi_moe_route, writes into the workspace (offsets from
- * mi_moe_workspace_layout) what mi_moe_run's sort writes: expert_off int32[33]
- * (followed by the row-tile prefixes of T's default GEMM kernels),
+ * staged parity: from global top-k ids (int32 [T, top_k]) and weights (fp32
+ * [T, top_k]), e.g. those of mi_moe_route, writes into the workspace (offsets
+ * from mi_moe_workspace_layout) what mi_moe_run's sort writes: expert_off
+ * int32[E+1] (followed by the row-tile prefixes of T's default GEMM kernels),
  * sorted_tok / sorted_w [S] (slots grouped by local expert, token-ascending
  * inside an expert) and tok_slot int32 [T, 8] (a token's slots in ascending
  * local expert, then -1). Ids outside [local_expert_offset,
- * local_expert_offset + 32) are not local. topk pointers 16-byte aligned,
- * workspace 256-byte aligned and at least mi_moe_workspace_size(T) bytes. */
+ * local_expert_offset + E) are not local. topk pointers 16-byte aligned when
+ * top_k = 8, else 4-byte; workspace 256-byte aligned and at least
+ * mi_moe_workspace_size(T) bytes. */
 int mi_moe_sort(const int32_t* topk_ids, const float* topk_weights, int64_t num_tokens,
                 int64_t local_expert_offset, void* workspace, size_t workspace_bytes, void* stream);
 
@@ -141,6 +150,22 @@ int mi_moe_sort(const int32_t* topk_ids, const float* topk_weights, int64_t num_
  * kernel.py:600-613. Pointers 16-byte aligned (scale: 4-byte). */
 int mi_moe_quantize_fp8(const void* hidden_bf16, int64_t num_tokens, uint8_t* hidden_states,
                         float* hidden_states_scale, void* stream);
+
+/* The definition this library is compiled for: the reference hard-codes it
+ * (kernel.py:615-625) and its routing kernel takes E_GLOBAL, N_GROUP,
+ * TOPK_GROUP and TOP_K as constexpr parameters (kernel.py:371-389);
+ * libmi_moe.so is moe_fp8_block_scale_ds_routing_topk8_ng8_kg4_e32_h7168_i2048,
+ * the other builds are named by their fields. */
+typedef struct mi_moe_definition {
+    int32_t hidden_size;        /* H */
+    int32_t intermediate_size;  /* I */
+    int32_t num_local_experts;  /* E: 16, 32 or 64 */
+    int32_t num_experts;        /* G: 64, 128 or 256 */
+    int32_t n_group;            /* routing groups of G / n_group experts */
+    int32_t topk_group;         /* groups kept per token */
+    int32_t top_k;              /* experts per token, <= 8 */
+} mi_moe_definition;
+int mi_moe_get_definition(mi_moe_definition* out);
 
 /* Hidden size H and expert intermediate size I this library is compiled for
  * (kernel.py:615-625 hard-codes 7168 and 2048; libmi_moe.so is that shape,

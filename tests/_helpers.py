@@ -17,24 +17,25 @@ def log(msg: str) -> None:
     print(f"[{time.strftime('%H:%M:%S')}] {msg}", file=sys.stderr, flush=True)
 
 
-def device_weights(device="cuda", H=W.H_DEF, I=W.I_DEF):
-    """Device copies of the seeded weights of shape (H, I), one per device and
-    shape; a second shape evicts the first (only one fits comfortably)."""
-    key = (device, H, I)
+def device_weights(device="cuda", H=W.H_DEF, I=W.I_DEF, E_local=W.E_LOCAL_DEF):
+    """Device copies of the seeded weights of shape (H, I) for E_local experts,
+    one set per device; another shape evicts the previous one."""
+    key = (device, H, I, E_local)
     if key not in _DEV_WEIGHTS:
         for k in [k for k in _DEV_WEIGHTS if k[0] == device]:
             del _DEV_WEIGHTS[k]
         t0 = time.time()
-        w = W.make_weights(H, I)
+        w = W.make_weights(H, I, E_local)
         _DEV_WEIGHTS[key] = {k: v.to(device) for k, v in w.items()}
-        log(f"weights (H={H}, I={I}) generated and copied in {time.time() - t0:.1f}s")
+        log(f"weights (H={H}, I={I}, {E_local} experts) generated and copied in "
+            f"{time.time() - t0:.1f}s")
     return _DEV_WEIGHTS[key]
 
 
 def gpu_args(wl: W.Workload, device="cuda"):
     t = wl.tensors
     w1 = t["gemm1_weights"]
-    dw = device_weights(device, int(w1.shape[2]), int(w1.shape[1]) // 2)
+    dw = device_weights(device, int(w1.shape[2]), int(w1.shape[1]) // 2, int(w1.shape[0]))
     return [t["routing_logits"].to(device), t["routing_bias"].to(device),
             t["hidden_states"].to(device), t["hidden_states_scale"].to(device),
             dw["gemm1_weights"], dw["gemm1_weights_scale"], dw["gemm2_weights"],
@@ -62,7 +63,8 @@ def subset_args(wl: W.Workload, tokens: torch.Tensor):
 
 def oracle_subset(wl: W.Workload, tokens: torch.Tensor):
     from oracle import ref_moe as R
-    return R.moe_forward(*subset_args(wl, tokens))
+    ng, kg, k = wl.routing
+    return R.moe_forward(*subset_args(wl, tokens), n_group=ng, topk_group=kg, top_k=k)
 
 
 def spread_tokens(T: int, n: int) -> torch.Tensor:

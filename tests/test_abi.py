@@ -226,6 +226,48 @@ def test_each_shape_library_reports_shape_and_exports(shape):
     assert lay.total - lay.part >= 800 * shape[0] * 2
 
 
+@pytest.mark.parametrize("defn", __import__("flashinfer_amd.shapes", fromlist=["x"]).DEFINITIONS,
+                         ids=lambda d: d.tag)
+def test_each_definition_library(defn):
+    """Every definition's library reports that definition, exports the whole
+    declared ABI, and sizes its workspace by top_k slots per token and its
+    local experts."""
+    from flashinfer_amd import shapes
+    assert shapes.definition_supported(defn)
+    L = _lib.lib(defn)
+    got = _lib.MiMoeDefinition()
+    assert L.mi_moe_get_definition(ctypes.byref(got)) == _lib.MI_MOE_OK
+    assert (got.hidden_size, got.intermediate_size, got.num_local_experts, got.num_experts,
+            got.n_group, got.topk_group, got.top_k) == (defn.H, defn.I, defn.EL, defn.EG, defn.NG,
+                                                        defn.KG, defn.TOPK)
+    assert f"e{defn.EL} g{defn.EG} ng{defn.NG} kg{defn.KG} k{defn.TOPK}" in L.mi_moe_version().decode()
+    for name in _declared_functions():
+        assert hasattr(L, name), name
+    T = 100
+    lay = _lib.workspace_layout(T, defn)
+    assert lay.part - lay.act >= T * defn.TOPK * defn.I * 2      # act rows for top_k*T slots
+    assert lay.total - lay.part >= T * defn.TOPK * defn.H * 2
+    assert lay.tok_slot - lay.sorted_w >= T * defn.TOPK * 4
+    assert lay.expert_off - lay.topk_w >= T * 8 * 4              # top-k rows are 8 wide
+    assert lay.sorted_tok - lay.expert_off >= 3 * _lib.meta_stride(defn) * 4
+    assert _lib.meta_stride(defn) >= defn.EL + 1
+    assert _lib.definition_for(defn.H, defn.I, defn.EL, defn.EG) == defn
+
+
+def test_definition_registry_rejects_unsupported():
+    from flashinfer_amd import shapes
+    D = shapes.Definition
+    assert not shapes.definition_supported(D(7168, 2048, EL=48))
+    assert not shapes.definition_supported(D(7168, 2048, EG=160, NG=8))     # not 64-lane whole
+    assert not shapes.definition_supported(D(7168, 2048, EG=256, NG=2))     # 32 lanes per group
+    assert shapes.definition_supported(D(7168, 2048, EG=256, NG=4))         # 16 lanes per group
+    assert not shapes.definition_supported(D(7168, 2048, TOPK=9))
+    assert not shapes.definition_supported(D(7168, 2048, KG=9))
+    assert shapes.definition_supported(D(7168, 2048, EG=64, NG=8, KG=2, TOPK=4, EL=16))
+    with pytest.raises(ValueError, match="no library"):
+        _lib.definition_for(7168, 2048, 16, 64)
+
+
 def test_unbuilt_shape_is_refused():
     with pytest.raises(ValueError, match="no library"):
         _lib.lib((2048, 768))

@@ -70,22 +70,46 @@ def test_route_skew_known_answer():
     assert torch.allclose(r.weights.double(), want, rtol=1e-6)
 
 
-def _brute_route(logits, bias, rsf):
+def _brute_route(logits, bias, rsf, n_group=None, topk_group=None, top_k=None):
     """Pure-Python selection on the same fp32 sigmoid values."""
+    n_group, topk_group, top_k = n_group or G, topk_group or KG, top_k or K
+    n_exp = logits.shape[1]
+    gsize = n_exp // n_group
     s = torch.sigmoid(logits.float())
     sb = (s + bias.float()[None, :])
     out_ids, out_w = [], []
     for t in range(logits.shape[0]):
         row = sb[t].tolist()
         gscore = []
-        for g in range(G):
-            vals = sorted(row[g * 32:(g + 1) * 32], reverse=True)
+        for g in range(n_group):
+            vals = sorted(row[g * gsize:(g + 1) * gsize], reverse=True)
             gscore.append(torch.tensor(vals[0], dtype=torch.float32) + torch.tensor(vals[1], dtype=torch.float32))
-        groups = sorted(range(G), key=lambda g: (-float(gscore[g]), g))[:KG]
-        cand = [e for e in range(E) if e // 32 in groups]
-        ids = sorted(cand, key=lambda e: (-row[e], e))[:K]
+        groups = sorted(range(n_group), key=lambda g: (-float(gscore[g]), g))[:topk_group]
+        cand = [e for e in range(n_exp) if e // gsize in groups]
+        ids = sorted(cand, key=lambda e: (-row[e], e))[:top_k]
         out_ids.append(ids)
     return out_ids
+
+
+@pytest.mark.parametrize("n_exp,n_group,topk_group,top_k", [(128, 8, 3, 6), (256, 4, 2, 8),
+                                                            (64, 8, 4, 4)])
+def test_route_other_definitions_brute_force(n_exp, n_group, topk_group, top_k):
+    """The routing restatement for other definitions of the family (the
+    reference's constexpr E_GLOBAL / N_GROUP / TOPK_GROUP / TOP_K,
+    kernel.py:371-389) against the pure-Python selection, plus its
+    invariants: top_k distinct ids from at most topk_group groups, weights
+    summing to the scaling factor."""
+    tok = W.make_tokens(80, seed=11, E_global=n_exp)
+    logits, bias = tok["routing_logits"], tok["routing_bias"]
+    r = R.route(logits, bias, 2.5, n_group, topk_group, top_k)
+    brute = _brute_route(logits, bias, 2.5, n_group, topk_group, top_k)
+    assert [sorted(x) for x in r.ids.tolist()] == [sorted(x) for x in brute]
+    gsize = n_exp // n_group
+    for t in range(80):
+        ids = r.ids[t].tolist()
+        assert len(set(ids)) == top_k
+        assert len({i // gsize for i in ids}) <= topk_group
+        assert abs(float(r.weights[t].sum()) - 2.5) < 1e-5
 
 
 def test_route_brute_force_and_invariants():
