@@ -70,7 +70,7 @@ class MiMoeDefinition(ctypes.Structure):
 class MiMoeLayout(ctypes.Structure):
     _fields_ = [(n, ctypes.c_size_t) for n in
                 ("topk_ids", "topk_w", "expert_off", "sorted_tok", "sorted_w", "tok_slot",
-                 "chunk_cnt", "act", "part", "total")]
+                 "chunk_cnt", "act", "part", "act_lo", "total")]
 
 
 _libs: dict = {}

@@ -46,6 +46,12 @@ static_assert((uint64_t)kMaxTokens * TOPK * I * 2 <= (1ull << 32), "GEMM2 tile r
 
 constexpr size_t align_up(size_t x) { return (x + 255) & ~(size_t)255; }
 
+// Largest T whose GEMM2 writes fp32 partial rows (and may run on the split
+// activation act + act_lo): the workspace reserves fp32 partials and act_lo
+// for these T. Up to here the call streams weights from HBM, and the wider
+// partials cost about 0.5% of the call.
+constexpr int64_t F32_PART_MAX_T = 256;
+
 constexpr mi_moe_layout make_layout(int64_t T) {
     mi_moe_layout L{};
     const size_t t = (size_t)(T < 0 ? 0 : T);
@@ -58,8 +64,10 @@ constexpr mi_moe_layout make_layout(int64_t T) {
     L.sorted_w = o;   o = align_up(o + s_max * 4);
     L.tok_slot = o;   o = align_up(o + t * TOPK_LD * 4);
     L.chunk_cnt = o;  o = align_up(o + (size_t)sort_chunks((int)t) * EL * 4);
+    const bool split = (int64_t)t <= F32_PART_MAX_T;
     L.act = o;        o = align_up(o + s_max * I * 2);
-    L.part = o;       o = align_up(o + s_max * H * 2);
+    L.part = o;       o = align_up(o + s_max * H * (split ? 4 : 2));
+    L.act_lo = o;     o = align_up(o + (split ? s_max * I * 2 : 0));
     L.total = o;
     return L;
 }
@@ -136,6 +144,8 @@ Plan make_plan(void* workspace, const mi_moe_layout& L, int64_t T, int64_t local
     p.chunk_cnt = (int*)(ws + L.chunk_cnt);
     p.act = (uint16_t*)(ws + L.act);
     p.part = (uint16_t*)(ws + L.part);
+    p.part_f32 = nullptr;
+    p.act_lo = nullptr;
     return p;
 }
 
@@ -165,6 +175,17 @@ constexpr int64_t ROUTE_IN_GEMM1_MAX_T = 1;
 int env_flag(const char* name) {  // -1 unset, else 0 / 1
     const char* v = getenv(name);
     return (v && *v) ? (atoi(v) != 0) : -1;
+}
+
+// GEMM2's inputs and outputs (G2_*): fp32 partial rows up to F32_PART_MAX_T
+// tokens with every GEMM2 kernel but the LDS tiles (MI_MOE_F32_PARTIALS=0
+// turns them off); the split activation only when MI_MOE_SPLIT_ACT=1 asks
+// for it (measured on MI355X it adds 5-9% at T = 1, 4, 64 and 256, 1.6% at
+// T = 16: the second operand's loads and registers cost occupancy).
+int gemm2_mode_for(int64_t T, int g2) {
+    if (T > F32_PART_MAX_T || g2 == 3 || g2 == 4 || g2 == 18) return G2_BF16;
+    if (env_flag("MI_MOE_SPLIT_ACT") == 1) return G2_SPLIT;
+    return env_flag("MI_MOE_F32_PARTIALS") == 0 ? G2_BF16 : G2_F32;
 }
 
 Front pick_front(int64_t T, int g1) {
@@ -389,6 +410,9 @@ static int run_impl(const mi_moe_args* a, hipStream_t s, hipEvent_t const* ev,
     Plan p = make_plan(a->workspace, L, T, a->local_expert_offset, a->routed_scaling_factor);
 
     const Variants var = pick_variants(T);
+    const int g2_mode = gemm2_mode_for(T, var.g2);
+    if (g2_mode != G2_BF16) p.part_f32 = (float*)p.part;
+    if (g2_mode == G2_SPLIT) p.act_lo = (uint16_t*)((uint8_t*)a->workspace + L.act_lo);
     hipError_t err = hipSuccess;
     auto mark = [&](int i) {
         if (ev && err == hipSuccess) err = hipEventRecord(ev[i], s);

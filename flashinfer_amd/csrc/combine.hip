@@ -4,7 +4,8 @@
 // fp32 atomic_add, so its summation order varies run to run), the fp32
 // zero-fill at :801, the bf16 cast at :820-823 and the empty-routing
 // zero_() at :692-695. Each token gathers its <= 8 slot rows (already
-// weighted by GEMM2's epilogue, bf16) in ascending local-expert order
+// weighted by GEMM2's epilogue; bf16, or fp32 when GEMM2 wrote part_f32) in
+// ascending local-expert order
 // (tok_slot from the sort kernel) and sums them in fp32 in that fixed order;
 // tokens with no local slot get zeros.
 // Every output row is written exactly once, so results are bit-identical
@@ -16,25 +17,35 @@ namespace mimoe {
 // Grid (T, H / 1024): one workgroup per token and 1024-column chunk; each
 // thread owns 4 columns and issues the loads of all its <= 8 slot rows
 // before summing them, so a call costs about one memory round trip.
+template <bool F32>
 __global__ __launch_bounds__(256) void combine_kernel(Plan p, uint16_t* __restrict__ out) {
     const int t = blockIdx.x;
     const int c = blockIdx.y * 1024 + threadIdx.x * 4;
     const int4 s0 = reinterpret_cast<const int4*>(p.tok_slot + (size_t)t * TOPK_LD)[0];
     const int4 s1 = reinterpret_cast<const int4*>(p.tok_slot + (size_t)t * TOPK_LD)[1];
     const int slot[8] = {s0.x, s0.y, s0.z, s0.w, s1.x, s1.y, s1.z, s1.w};
-    uint2 v[8];
+    float4 v[8];
 #pragma unroll
-    for (int j = 0; j < TOPK; ++j)
-        v[j] = slot[j] >= 0 ? *reinterpret_cast<const uint2*>(p.part + (size_t)slot[j] * H + c)
-                            : make_uint2(0u, 0u);
+    for (int j = 0; j < TOPK; ++j) {
+        if constexpr (F32) {
+            v[j] = slot[j] >= 0 ? *reinterpret_cast<const float4*>(p.part_f32 + (size_t)slot[j] * H + c)
+                                : make_float4(0.f, 0.f, 0.f, 0.f);
+        } else {
+            const uint2 u = slot[j] >= 0
+                                ? *reinterpret_cast<const uint2*>(p.part + (size_t)slot[j] * H + c)
+                                : make_uint2(0u, 0u);
+            v[j] = make_float4(bf2f(u.x & 0xffffu), bf2f(u.x >> 16), bf2f(u.y & 0xffffu),
+                               bf2f(u.y >> 16));
+        }
+    }
     float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
 #pragma unroll
     for (int j = 0; j < TOPK; ++j) {
         if (slot[j] < 0) break;
-        acc.x += bf2f(v[j].x & 0xffffu);
-        acc.y += bf2f(v[j].x >> 16);
-        acc.z += bf2f(v[j].y & 0xffffu);
-        acc.w += bf2f(v[j].y >> 16);
+        acc.x += v[j].x;
+        acc.y += v[j].y;
+        acc.z += v[j].z;
+        acc.w += v[j].w;
     }
     uint2 o;
     o.x = (uint32_t)f2bf(acc.x) | ((uint32_t)f2bf(acc.y) << 16);
@@ -44,7 +55,10 @@ __global__ __launch_bounds__(256) void combine_kernel(Plan p, uint16_t* __restri
 
 hipError_t launch_combine(const Plan& p, uint16_t* out, hipStream_t s) {
     if (p.T <= 0) return hipSuccess;
-    hipLaunchKernelGGL(combine_kernel, dim3(p.T, H / 1024), dim3(256), 0, s, p, out);
+    if (p.part_f32)
+        hipLaunchKernelGGL(combine_kernel<true>, dim3(p.T, H / 1024), dim3(256), 0, s, p, out);
+    else
+        hipLaunchKernelGGL(combine_kernel<false>, dim3(p.T, H / 1024), dim3(256), 0, s, p, out);
     return hipGetLastError();
 }
 

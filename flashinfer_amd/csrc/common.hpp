@@ -87,7 +87,24 @@ struct Plan {
     int* chunk_cnt;            // [ceil(T/1024), EL] per-chunk expert totals (large-T sort)
     uint16_t* act;             // bf16 [TOPK*T, I]
     uint16_t* part;            // bf16 [TOPK*T, H]: routing weight x GEMM2 row of each slot
+    // part_f32 (the same bytes as part), when set: GEMM2 writes the weighted
+    // rows in fp32 there and the combine sums those, as the reference's
+    // fp32 partials (kernel.py:364-368).
+    float* part_f32;           // fp32 [TOPK*T, H] or null
+    // act_lo (only with part_f32), when set: GEMM1 also writes
+    // bf16(x - bf16(x)) of each SwiGLU value x there, and GEMM2 multiplies
+    // act + act_lo, 16 mantissa bits (the reference's fp32 -> TF32 operand
+    // keeps 10, kernel.py:272-278).
+    uint16_t* act_lo;          // bf16 [TOPK*T, I] or null
 };
+
+// What a GEMM2 kernel reads and writes (template argument, picked per call).
+constexpr int G2_BF16 = 0;   // act; bf16 rows to part
+constexpr int G2_F32 = 1;    // act; fp32 rows to part_f32
+constexpr int G2_SPLIT = 2;  // act + act_lo; fp32 rows to part_f32
+inline int gemm2_mode(const Plan& p) {
+    return p.act_lo ? G2_SPLIT : (p.part_f32 ? G2_F32 : G2_BF16);
+}
 
 constexpr int META_STRIDE = EL < 64 ? 64 : 128;  // holds EL + 1 entries
 constexpr int META_EXPERT_OFF = 0;
@@ -137,6 +154,14 @@ __device__ __forceinline__ v4i fp8x8_to_bf16x8(uint32_t w0, uint32_t w1) {
 }
 
 __device__ __forceinline__ float silu(float x) { return x / (1.0f + __expf(-x)); }
+
+// One SwiGLU value into act (bf16, round to nearest even) and, for the
+// exact-input GEMM2, the remainder into act_lo.
+__device__ __forceinline__ void store_act(const Plan& p, size_t idx, float v) {
+    const uint16_t hi = f2bf(v);
+    p.act[idx] = hi;
+    if (p.act_lo) p.act_lo[idx] = f2bf(v - bf2f(hi));
+}
 
 __device__ __forceinline__ int lane_id() { return __lane_id(); }
 

@@ -209,7 +209,7 @@ void gemm1_stream_kernel(Plan p, const uint8_t* __restrict__ hs, const float* __
             const int m = i * 16 + g * 4 + rr;
             if (m < nrows) {
                 const float v = silu(accu[i][rr]) * accg[i][rr];
-                p.act[(size_t)(row0 + m) * I + j0 + r] = f2bf(v);
+                store_act(p, (size_t)(row0 + m) * I + j0 + r, v);
             }
         }
     }

@@ -191,7 +191,7 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm1_tile_kernel(
                 const int row = wm * 64 + m * 16 + g * 4 + i;
                 if (row < nrows) {
                     const float v = silu(acc[m][n + 4][i]) * acc[m][n][i];
-                    p.act[(size_t)(row0 + row) * I + jb + wn * 64 + n * 16 + r] = f2bf(v);
+                    store_act(p, (size_t)(row0 + row) * I + jb + wn * 64 + n * 16 + r, v);
                 }
             }
         }
@@ -377,15 +377,18 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm1_tile_t_kernel(
         if (row < nrows) {
 #pragma unroll
             for (int n = 0; n < 4; ++n) {
-                uint32_t w[2];
+                uint32_t w[2], wl[2];
 #pragma unroll
                 for (int h = 0; h < 2; ++h) {
                     const float v0 = silu(acc[n + 4][m][2 * h]) * acc[n][m][2 * h];
                     const float v1 = silu(acc[n + 4][m][2 * h + 1]) * acc[n][m][2 * h + 1];
-                    w[h] = (uint32_t)f2bf(v0) | ((uint32_t)f2bf(v1) << 16);
+                    const uint16_t h0 = f2bf(v0), h1 = f2bf(v1);
+                    w[h] = (uint32_t)h0 | ((uint32_t)h1 << 16);
+                    wl[h] = (uint32_t)f2bf(v0 - bf2f(h0)) | ((uint32_t)f2bf(v1 - bf2f(h1)) << 16);
                 }
-                *reinterpret_cast<uint2*>(p.act + (size_t)(row0 + row) * I + jb + wn * 64 + n * 16 +
-                                          4 * g) = make_uint2(w[0], w[1]);
+                const size_t idx = (size_t)(row0 + row) * I + jb + wn * 64 + n * 16 + 4 * g;
+                *reinterpret_cast<uint2*>(p.act + idx) = make_uint2(w[0], w[1]);
+                if (p.act_lo) *reinterpret_cast<uint2*>(p.act_lo + idx) = make_uint2(wl[0], wl[1]);
             }
         }
     }

@@ -298,7 +298,7 @@ __global__ __launch_bounds__(64 * WIDE_NW) void gemm1_wide_kernel(Plan p, const 
             const int row = m * 16 + g * 4 + i;
             if (row < nrows) {
                 const float v = silu(accu[m][i]) * accg[m][i];
-                p.act[(size_t)(row0 + row) * I + j0 + r] = f2bf(v);
+                store_act(p, (size_t)(row0 + row) * I + j0 + r, v);
             }
         }
     }

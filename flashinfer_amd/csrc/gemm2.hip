@@ -9,12 +9,16 @@
 // v_mfma_f32_16x16x32_bf16; the 128-block weight scale multiplies each
 // block's partial sum in fp32. The activation stays bf16 rather than being
 // requantised to fp8, whose 3-bit mantissa would put the output outside a
-// 1e-2 relative tolerance.
+// 1e-2 relative tolerance. At decode sizes (where the call is HBM-bound and
+// the MFMAs idle) the activation is split into bf16 hi + lo, which is wider
+// than the reference's TF32 operand, and the partial rows are fp32.
 //
-// Stream variant (template <MT, D, NW, NQ>): NW waves per workgroup, each
-// owning NQ 16-column sub-tiles (16 * NQ output columns, inside one 128-column
-// scale block) for 16 * MT slots of one expert; weights go global -> VGPR
-// through a D-deep prefetch ring.
+// Stream variant (template <MT, D, NW, NQ, MODE>): NW waves per workgroup,
+// each owning NQ 16-column sub-tiles (16 * NQ output columns, inside one
+// 128-column scale block) for 16 * MT slots of one expert; weights go
+// global -> VGPR through a D-deep prefetch ring. MODE (G2_*): the weighted
+// rows go to part (bf16) or part_f32, and with G2_SPLIT the activation is
+// act + act_lo (two bf16 MFMAs per k step against the same bf16 weights).
 //
 // Operand layout: lane l (row l % 16, g = l / 16) loads bytes [16g, 16g+16)
 // and [64+16g, 64+16g+16) of the 128-wide k-block of its weight row; MFMA h
@@ -40,12 +44,21 @@ __device__ __forceinline__ Frag16 ld_act(const uint16_t* row, int kb, int g) {
     return f;
 }
 
-__device__ __forceinline__ v4f mfma_block(const Frag16& a, const v8i& b) {
+// One 128-deep k-block of a 16 x 16 tile: a . b (+ al . b with PREC, the
+// small remainder first).
+template <bool PREC>
+__device__ __forceinline__ v4f mfma_block(const Frag16& a, const Frag16& al, const v8i& b) {
     v4f acc = {0.f, 0.f, 0.f, 0.f};
     const v4i b0 = fp8x8_to_bf16x8((uint32_t)b.s0, (uint32_t)b.s1);
     const v4i b1 = fp8x8_to_bf16x8((uint32_t)b.s2, (uint32_t)b.s3);
     const v4i b2 = fp8x8_to_bf16x8((uint32_t)b.s4, (uint32_t)b.s5);
     const v4i b3 = fp8x8_to_bf16x8((uint32_t)b.s6, (uint32_t)b.s7);
+    if constexpr (PREC) {  // one chain: the NQ sub-tiles of a wave give the MFMAs their overlap
+        acc = mfma_bf16_16x16x32(__builtin_bit_cast(v8bf, al.c0), __builtin_bit_cast(v8bf, b0), acc);
+        acc = mfma_bf16_16x16x32(__builtin_bit_cast(v8bf, al.c1), __builtin_bit_cast(v8bf, b1), acc);
+        acc = mfma_bf16_16x16x32(__builtin_bit_cast(v8bf, al.c2), __builtin_bit_cast(v8bf, b2), acc);
+        acc = mfma_bf16_16x16x32(__builtin_bit_cast(v8bf, al.c3), __builtin_bit_cast(v8bf, b3), acc);
+    }
     acc = mfma_bf16_16x16x32(__builtin_bit_cast(v8bf, a.c0), __builtin_bit_cast(v8bf, b0), acc);
     acc = mfma_bf16_16x16x32(__builtin_bit_cast(v8bf, a.c1), __builtin_bit_cast(v8bf, b1), acc);
     acc = mfma_bf16_16x16x32(__builtin_bit_cast(v8bf, a.c2), __builtin_bit_cast(v8bf, b2), acc);
@@ -53,11 +66,12 @@ __device__ __forceinline__ v4f mfma_block(const Frag16& a, const v8i& b) {
     return acc;
 }
 
-template <int MT, int D, int NW, int NQ>
-__global__ __launch_bounds__(64 * NW) void gemm2_stream_kernel(Plan p, const uint8_t* __restrict__ w2,
-                                                               const float* __restrict__ w2s) {
+template <int MT, int D, int NW, int NQ, int MODE>
+__global__ __launch_bounds__(64 * NW) void gemm2_stream_kernel(
+    Plan p, const uint8_t* __restrict__ w2, const float* __restrict__ w2s) {
     static_assert(BLK % (16 * NQ) == 0, "a wave's columns stay inside one scale block");
     static_assert(IB % D == 0, "prefetch depth must divide the k-block count");
+    constexpr bool PREC = MODE == G2_SPLIT;
     constexpr int BM = 16 * MT;
     int e, row0, nrows;
     if (!find_tile(p.meta, META_MTILE2, blockIdx.y, BM, e, row0, nrows)) return;
@@ -73,12 +87,18 @@ __global__ __launch_bounds__(64 * NW) void gemm2_stream_kernel(Plan p, const uin
 #pragma unroll
     for (int q = 0; q < NQ; ++q) b_ptr[q] = w2 + ((size_t)e * H + n0 + q * 16 + r) * I + g * 16;
     const uint16_t* a_row[MT];
+    const uint16_t* al_row[MT];
 #pragma unroll
-    for (int i = 0; i < MT; ++i) a_row[i] = p.act + (size_t)(row0 + min(i * 16 + r, nrows - 1)) * I;
+    for (int i = 0; i < MT; ++i) {
+        const size_t off = (size_t)(row0 + min(i * 16 + r, nrows - 1)) * I;
+        a_row[i] = p.act + off;
+        al_row[i] = PREC ? p.act_lo + off : nullptr;
+    }
     const float* sb_ptr = w2s + ((size_t)e * HB + nb) * IB;
 
     v8i b[D][NQ];
     Frag16 a[D][MT];
+    Frag16 al[D][MT];  // PREC only
     v4f acc[MT][NQ];
     const v4f zero = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
@@ -92,7 +112,7 @@ __global__ __launch_bounds__(64 * NW) void gemm2_stream_kernel(Plan p, const uin
         for (int i = 0; i < MT; ++i) {
 #pragma unroll
             for (int q = 0; q < NQ; ++q) {
-                const v4f pr = mfma_block(a[d][i], b[d][q]);
+                const v4f pr = mfma_block<PREC>(a[d][i], al[d][i], b[d][q]);
                 acc[i][q][0] += pr[0] * sb;
                 acc[i][q][1] += pr[1] * sb;
                 acc[i][q][2] += pr[2] * sb;
@@ -104,7 +124,10 @@ __global__ __launch_bounds__(64 * NW) void gemm2_stream_kernel(Plan p, const uin
 #pragma unroll
         for (int q = 0; q < NQ; ++q) b[d][q] = ld_frag(b_ptr[q] + kb * BLK);
 #pragma unroll
-        for (int i = 0; i < MT; ++i) a[d][i] = ld_act(a_row[i], kb, g);
+        for (int i = 0; i < MT; ++i) {
+            a[d][i] = ld_act(a_row[i], kb, g);
+            if constexpr (PREC) al[d][i] = ld_act(al_row[i], kb, g);
+        }
     };
 
 #pragma unroll
@@ -133,7 +156,7 @@ __global__ __launch_bounds__(64 * NW) void gemm2_stream_kernel(Plan p, const uin
         for (int rr = 0; rr < 4; ++rr) asm volatile("" : "+v"(wrow[i][rr]));
 
     // Epilogue: weight each slot's row by its routing weight (kernel.py:364)
-    // and store bf16 for the combine.
+    // and store it (bf16, or fp32 unless G2_BF16) for the combine.
 #pragma unroll
     for (int i = 0; i < MT; ++i) {
 #pragma unroll
@@ -141,9 +164,12 @@ __global__ __launch_bounds__(64 * NW) void gemm2_stream_kernel(Plan p, const uin
             const int m = i * 16 + g * 4 + rr;
             if (m < nrows) {
                 const float w = wrow[i][rr];
-                uint16_t* dst = p.part + (size_t)(row0 + m) * H + n0 + r;
+                const size_t o = (size_t)(row0 + m) * H + n0 + r;
 #pragma unroll
-                for (int q = 0; q < NQ; ++q) dst[16 * q] = f2bf(w * acc[i][q][rr]);
+                for (int q = 0; q < NQ; ++q) {
+                    if constexpr (MODE != G2_BF16) p.part_f32[o + 16 * q] = w * acc[i][q][rr];
+                    else p.part[o + 16 * q] = f2bf(w * acc[i][q][rr]);
+                }
             }
         }
     }
@@ -169,7 +195,19 @@ static void launch_stream2(const Plan& p, const uint8_t* w2, const float* w2s, h
     // a ring deeper than the shape's k-blocks allow falls back to 2 deep
     constexpr int DD = IB % D == 0 ? D : 2;
     dim3 grid(H / (16 * NQ * NW), max_mtiles(p.T, 16 * MT));
-    hipLaunchKernelGGL((gemm2_stream_kernel<MT, DD, NW, NQ>), grid, dim3(64 * NW), 0, s, p, w2, w2s);
+    switch (gemm2_mode(p)) {
+        case G2_SPLIT:
+            hipLaunchKernelGGL((gemm2_stream_kernel<MT, DD, NW, NQ, G2_SPLIT>), grid, dim3(64 * NW), 0, s,
+                               p, w2, w2s);
+            break;
+        case G2_F32:
+            hipLaunchKernelGGL((gemm2_stream_kernel<MT, DD, NW, NQ, G2_F32>), grid, dim3(64 * NW), 0, s,
+                               p, w2, w2s);
+            break;
+        default:
+            hipLaunchKernelGGL((gemm2_stream_kernel<MT, DD, NW, NQ, G2_BF16>), grid, dim3(64 * NW), 0, s,
+                               p, w2, w2s);
+    }
 }
 
 hipError_t launch_gemm2(const Plan& p, const uint8_t* w2, const float* w2s, int variant,

@@ -15,7 +15,8 @@
 // read-modify-write is race-free). After a barrier the 4 per-wave
 // accumulators are summed in wave order and written as bf16; tokens with no
 // local slot get zeros. Every summation order is fixed, so results are
-// bit-identical across runs.
+// bit-identical across runs. PREC: the activation is act + act_lo, each k
+// step runs the MFMAs of both bf16 halves against the same weights.
 #include "common.hpp"
 
 namespace mimoe {
@@ -36,7 +37,7 @@ __device__ __forceinline__ UnitInfo unit_info(const int* meta, int u) {
     return r;
 }
 
-template <int D, int KS = 1>
+template <int D, int KS, bool PREC>
 __global__ __launch_bounds__(256) void gemm2_combine_kernel(Plan p, const uint8_t* __restrict__ w2,
                                                             const float* __restrict__ w2s,
                                                             uint16_t* __restrict__ out) {
@@ -69,6 +70,7 @@ __global__ __launch_bounds__(256) void gemm2_combine_kernel(Plan p, const uint8_
     if (nsteps > 0) {
         v8i b[D];
         v4i a[D][4];
+        v4i al[D][4];  // PREC only
         // Per-tile data, fetched when the load side enters a tile (D steps
         // before the compute side needs it): block scales of the 16 k-blocks,
         // and the token and routing weight of the lane's 4 output rows.
@@ -100,12 +102,19 @@ __global__ __launch_bounds__(256) void gemm2_combine_kernel(Plan p, const uint8_
             if (s % KBW == 0 && s > 0) fetch_unit(u0 + ustep * (s / KBW));
             const uint8_t* bp = w2 + ((size_t)lu.e * H + n0 + r) * I + g * 16 + kb * BLK;
             b[d] = ld_frag(bp);
-            const uint16_t* ap =
-                p.act + (size_t)(lu.row0 + min(r, lu.nrows - 1)) * I + kb * BLK + g * 16;
+            const size_t ao = (size_t)(lu.row0 + min(r, lu.nrows - 1)) * I + kb * BLK + g * 16;
+            const uint16_t* ap = p.act + ao;
             a[d][0] = ld16(ap);
             a[d][1] = ld16(ap + 8);
             a[d][2] = ld16(ap + 64);
             a[d][3] = ld16(ap + 72);
+            if constexpr (PREC) {
+                const uint16_t* lp = p.act_lo + ao;
+                al[d][0] = ld16(lp);
+                al[d][1] = ld16(lp + 8);
+                al[d][2] = ld16(lp + 64);
+                al[d][3] = ld16(lp + 72);
+            }
         };
         auto compute = [&](int d, int s) __attribute__((always_inline)) {
             const int kb = kb0 + s % KBW;
@@ -123,10 +132,18 @@ __global__ __launch_bounds__(256) void gemm2_combine_kernel(Plan p, const uint8_
             const v4i b1 = fp8x8_to_bf16x8((uint32_t)b[d].s2, (uint32_t)b[d].s3);
             const v4i b2 = fp8x8_to_bf16x8((uint32_t)b[d].s4, (uint32_t)b[d].s5);
             const v4i b3 = fp8x8_to_bf16x8((uint32_t)b[d].s6, (uint32_t)b[d].s7);
+            v4f pl = pr;  // PREC: the act_lo products, a chain of their own
+            if constexpr (PREC) {
+                pl = mfma_bf16_16x16x32(__builtin_bit_cast(v8bf, al[d][0]), __builtin_bit_cast(v8bf, b0), pl);
+                pl = mfma_bf16_16x16x32(__builtin_bit_cast(v8bf, al[d][1]), __builtin_bit_cast(v8bf, b1), pl);
+                pl = mfma_bf16_16x16x32(__builtin_bit_cast(v8bf, al[d][2]), __builtin_bit_cast(v8bf, b2), pl);
+                pl = mfma_bf16_16x16x32(__builtin_bit_cast(v8bf, al[d][3]), __builtin_bit_cast(v8bf, b3), pl);
+            }
             pr = mfma_bf16_16x16x32(__builtin_bit_cast(v8bf, a[d][0]), __builtin_bit_cast(v8bf, b0), pr);
             pr = mfma_bf16_16x16x32(__builtin_bit_cast(v8bf, a[d][1]), __builtin_bit_cast(v8bf, b1), pr);
             pr = mfma_bf16_16x16x32(__builtin_bit_cast(v8bf, a[d][2]), __builtin_bit_cast(v8bf, b2), pr);
             pr = mfma_bf16_16x16x32(__builtin_bit_cast(v8bf, a[d][3]), __builtin_bit_cast(v8bf, b3), pr);
+            if constexpr (PREC) pr += pl;
             acc[0] += pr[0] * sb;
             acc[1] += pr[1] * sb;
             acc[2] += pr[2] * sb;
@@ -173,7 +190,12 @@ hipError_t launch_gemm2_combine(const Plan& p, const uint8_t* w2, const float* w
     if (p.T <= 0) return hipSuccess;
     const size_t lds = (size_t)4 * p.T * 16 * sizeof(float);
     constexpr int D = IB % 4 == 0 ? 4 : 2;  // ring depth must divide the shape's k-blocks
-    hipLaunchKernelGGL((gemm2_combine_kernel<D>), dim3(H / 16), dim3(256), lds, s, p, w2, w2s, out);
+    if (p.act_lo)
+        hipLaunchKernelGGL((gemm2_combine_kernel<D, 1, true>), dim3(H / 16), dim3(256), lds, s, p, w2,
+                           w2s, out);
+    else
+        hipLaunchKernelGGL((gemm2_combine_kernel<D, 1, false>), dim3(H / 16), dim3(256), lds, s, p,
+                           w2, w2s, out);
     return hipGetLastError();
 }
 
@@ -183,8 +205,12 @@ hipError_t launch_gemm2_combine_ks(const Plan& p, const uint8_t* w2, const float
     const size_t lds = (size_t)4 * p.T * 16 * sizeof(float);
     constexpr int KBW = IB / 4;
     constexpr int D = (KBW % 2 == 0 && KBW > 2) ? 2 : 1;  // divides a wave's k-blocks, below them
-    hipLaunchKernelGGL((gemm2_combine_kernel<D, 4>), dim3(H / 16), dim3(256), lds, s, p, w2, w2s,
-                       out);
+    if (p.act_lo)
+        hipLaunchKernelGGL((gemm2_combine_kernel<D, 4, true>), dim3(H / 16), dim3(256), lds, s, p, w2,
+                           w2s, out);
+    else
+        hipLaunchKernelGGL((gemm2_combine_kernel<D, 4, false>), dim3(H / 16), dim3(256), lds, s, p,
+                           w2, w2s, out);
     return hipGetLastError();
 }
 

@@ -5,7 +5,7 @@
 //   part[s, n] = bf16(w_s * sum_kb sb2[e, n/128, kb] * (act[s, kb-block] . W2[e, n, kb-block]))
 // with bf16 activations and fp8 weights widened to bf16 (exact).
 //
-// Shape (template <MTW, D, DA>): a workgroup of 4 waves owns BM = 16*MTW
+// Shape (template <MTW, D, DA, MODE>): a workgroup of 4 waves owns BM = 16*MTW
 // slots of one expert and 64 output columns; wave w owns columns n0..n0+15
 // for all BM rows, so its 16 weight rows go global -> VGPR through a D-deep
 // register ring (no two waves share them). The BM activation rows of a
@@ -13,6 +13,9 @@
 // into a DA-deep register staging ring and written to an LDS double buffer
 // one k-block ahead of their use: one barrier per k-block. The 64 columns lie
 // in one 128-column scale block, so sb2 is one uniform value per k-block.
+// MODE (G2_*): rows go to part (bf16) or part_f32; with G2_SPLIT the act_lo
+// rows ride along as rows BM..2BM-1 of the LDS buffers and each k step runs
+// the MFMAs of both halves against the same bf16 weights.
 //
 // Operand k order (identical for A and B, so the pairing is exact): lane
 // (r = l%16, g = l/16) holds k-block offsets 16g+[0,16) and 64+16g+[0,16);
@@ -30,17 +33,19 @@ constexpr int W2_N = 16 * W2_NW;   // output columns per workgroup
 constexpr int W2_BM = 32;          // rows per workgroup (see the launcher)
 }  // namespace
 
-template <int MTW, int D, int DA>
+template <int MTW, int D, int DA, int MODE>
 __global__ __launch_bounds__(64 * W2_NW) void gemm2_wide_kernel(Plan p, const uint8_t* __restrict__ w2,
                                                                 const float* __restrict__ w2s) {
+    constexpr bool PREC = MODE == G2_SPLIT;
     constexpr int BM = 16 * MTW;
+    constexpr int AROWS = PREC ? 2 * BM : BM;         // LDS rows: act (and act_lo)
     constexpr int THREADS = 64 * W2_NW;
     constexpr int ROW_BYTES = BLK * 2;                // one k-block of a bf16 row
     constexpr int ROWS_PER_PASS = THREADS / 16;       // 16 threads x 16 B cover one row
-    constexpr int A_LD = BM / ROWS_PER_PASS;          // 16-byte loads per thread per k-block
+    constexpr int A_LD = AROWS / ROWS_PER_PASS;       // 16-byte loads per thread per k-block
     static_assert(BM % ROWS_PER_PASS == 0 && BM <= THREADS, "activation loader");
     static_assert(IB % D == 0 && IB % DA == 0 && D > DA, "ring depths");
-    __shared__ __attribute__((aligned(16))) uint8_t a_lds[2][BM * ROW_BYTES];
+    __shared__ __attribute__((aligned(16))) uint8_t a_lds[2][AROWS * ROW_BYTES];
     __shared__ float w_lds[THREADS];  // routing weights of the tile's slots (first BM used)
 
     int e, row0, nrows;
@@ -57,14 +62,15 @@ __global__ __launch_bounds__(64 * W2_NW) void gemm2_wide_kernel(Plan p, const ui
     const float* sb_ptr = w2s + ((size_t)e * HB + nb0 / BLK) * IB;
 
     // activation loader: thread t copies chunk t%16 of rows t/16 + 16i
-    const uint8_t* act = reinterpret_cast<const uint8_t*>(p.act);
     const int ac = tid & 15;
     const uint8_t* a_src[A_LD];
     uint32_t a_dst[A_LD];
 #pragma unroll
     for (int i = 0; i < A_LD; ++i) {
-        const int row = (tid >> 4) + ROWS_PER_PASS * i;
-        a_src[i] = act + (size_t)(row0 + min(row, nrows - 1)) * (I * 2) + ac * 16;
+        const int row = (tid >> 4) + ROWS_PER_PASS * i;  // LDS row: act rows, then act_lo rows
+        const int lo = row >= BM;
+        const uint8_t* act = reinterpret_cast<const uint8_t*>(lo ? p.act_lo : p.act);
+        a_src[i] = act + (size_t)(row0 + min(row - lo * BM, nrows - 1)) * (I * 2) + ac * 16;
         a_dst[i] = row * ROW_BYTES + ((ac ^ swz16(row)) << 4);
     }
     // Routing weights of the tile: loaded first, stored to LDS after the
@@ -103,10 +109,24 @@ __global__ __launch_bounds__(64 * W2_NW) void gemm2_wide_kernel(Plan p, const ui
             const v4i a1 = lds16(base + (((2 * g + 1) ^ sw) << 4));
             const v4i a2 = lds16(base + (((8 + 2 * g) ^ sw) << 4));
             const v4i a3 = lds16(base + (((9 + 2 * g) ^ sw) << 4));
+            v4f pl = zero;  // act_lo products: a chain of their own
+            if constexpr (PREC) {
+                // act_lo row m*16+r sits BM rows further (same swizzle: BM % 16 == 0)
+                const uint8_t* lbase = base + BM * ROW_BYTES;
+                const v4i l0 = lds16(lbase + (((2 * g) ^ sw) << 4));
+                const v4i l1 = lds16(lbase + (((2 * g + 1) ^ sw) << 4));
+                const v4i l2 = lds16(lbase + (((8 + 2 * g) ^ sw) << 4));
+                const v4i l3 = lds16(lbase + (((9 + 2 * g) ^ sw) << 4));
+                pl = mfma_bf16_16x16x32(__builtin_bit_cast(v8bf, l0), __builtin_bit_cast(v8bf, b0), pl);
+                pl = mfma_bf16_16x16x32(__builtin_bit_cast(v8bf, l1), __builtin_bit_cast(v8bf, b1), pl);
+                pl = mfma_bf16_16x16x32(__builtin_bit_cast(v8bf, l2), __builtin_bit_cast(v8bf, b2), pl);
+                pl = mfma_bf16_16x16x32(__builtin_bit_cast(v8bf, l3), __builtin_bit_cast(v8bf, b3), pl);
+            }
             v4f pr = mfma_bf16_16x16x32(__builtin_bit_cast(v8bf, a0), __builtin_bit_cast(v8bf, b0), zero);
             pr = mfma_bf16_16x16x32(__builtin_bit_cast(v8bf, a1), __builtin_bit_cast(v8bf, b1), pr);
             pr = mfma_bf16_16x16x32(__builtin_bit_cast(v8bf, a2), __builtin_bit_cast(v8bf, b2), pr);
             pr = mfma_bf16_16x16x32(__builtin_bit_cast(v8bf, a3), __builtin_bit_cast(v8bf, b3), pr);
+            if constexpr (PREC) pr += pl;
             acc[m][0] += pr[0] * sb; acc[m][1] += pr[1] * sb;
             acc[m][2] += pr[2] * sb; acc[m][3] += pr[3] * sb;
         }
@@ -152,7 +172,8 @@ __global__ __launch_bounds__(64 * W2_NW) void gemm2_wide_kernel(Plan p, const ui
         }
     }
 
-    // Epilogue: routing weight (kernel.py:364) and bf16 store for the combine.
+    // Epilogue: routing weight (kernel.py:364) and the store for the combine
+    // (bf16, or fp32 unless G2_BF16).
 #pragma unroll
     for (int m = 0; m < MTW; ++m) {
 #pragma unroll
@@ -160,7 +181,9 @@ __global__ __launch_bounds__(64 * W2_NW) void gemm2_wide_kernel(Plan p, const ui
             const int row = m * 16 + g * 4 + i;
             if (row < nrows) {
                 const float w = w_lds[row];
-                p.part[(size_t)(row0 + row) * H + n0 + r] = f2bf(w * acc[m][i]);
+                const size_t o = (size_t)(row0 + row) * H + n0 + r;
+                if constexpr (MODE != G2_BF16) p.part_f32[o] = w * acc[m][i];
+                else p.part[o] = f2bf(w * acc[m][i]);
             }
         }
     }
@@ -171,7 +194,20 @@ hipError_t launch_gemm2_wide(const Plan& p, const uint8_t* w2, const float* w2s,
     // 17 KB of LDS, so six workgroups per CU. Measured against 64- and
     // 128-row tiles and 4- and 8-deep rings.
     dim3 grid(H / W2_N, max_mtiles(p.T, W2_BM));
-    hipLaunchKernelGGL((gemm2_wide_kernel<W2_BM / 16, 2, 1>), grid, dim3(64 * W2_NW), 0, s, p, w2, w2s);
+    constexpr int MTW = W2_BM / 16;
+    switch (gemm2_mode(p)) {
+        case G2_SPLIT:
+            hipLaunchKernelGGL((gemm2_wide_kernel<MTW, 2, 1, G2_SPLIT>), grid, dim3(64 * W2_NW), 0, s, p,
+                               w2, w2s);
+            break;
+        case G2_F32:
+            hipLaunchKernelGGL((gemm2_wide_kernel<MTW, 2, 1, G2_F32>), grid, dim3(64 * W2_NW), 0, s, p,
+                               w2, w2s);
+            break;
+        default:
+            hipLaunchKernelGGL((gemm2_wide_kernel<MTW, 2, 1, G2_BF16>), grid, dim3(64 * W2_NW), 0, s, p,
+                               w2, w2s);
+    }
     return hipGetLastError();
 }
 

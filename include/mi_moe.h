@@ -79,10 +79,17 @@ typedef struct mi_moe_args {
  *   sorted_w   fp32  [kT]     routing weight of each slot
  *   tok_slot   int32 [T, 8]   slots of each token, ascending local expert, -1 pad
  *   chunk_cnt  int32 [ceil(T/1024), E]  per-1024-token-chunk local expert counts
- *   act        bf16  [kT, 2048]  SwiGLU(GEMM1) per slot
- *   part       bf16  [kT, 7168]  routing weight x GEMM2 row per slot        */
+ *   act        bf16  [kT, 2048]  SwiGLU(GEMM1) per slot, rounded to bf16
+ *   part       bf16  [kT, 7168]  routing weight x GEMM2 row per slot; fp32
+ *                             (same offset, twice the bytes) at T <= 256
+ *   act_lo     bf16  [kT, 2048]  SwiGLU(GEMM1) - act, reserved at T <= 256
+ *                             (empty above) and written when the environment
+ *                             sets MI_MOE_SPLIT_ACT=1: GEMM2 then multiplies
+ *                             act + act_lo, 16 mantissa bits, wider than the
+ *                             reference's TF32 operand (kernel.py:272-278) */
 typedef struct mi_moe_layout {
     size_t topk_ids, topk_w, expert_off, sorted_tok, sorted_w, tok_slot, chunk_cnt, act, part;
+    size_t act_lo;
     size_t total;
 } mi_moe_layout;
 
@@ -181,7 +188,7 @@ int mi_moe_shape(int32_t* hidden_size, int32_t* intermediate_size);
  * tight serving loops, harnesses that forbid hipMalloc). No counterpart in
  * the reference. args->workspace must be NULL and args->workspace_bytes 0:
  * the intermediates live in the library's static device array (one per GPU,
- * mi_moe_workspace_size(MI_MOE_NOALLOC_MAX_TOKENS) bytes, about 38 MB at
+ * mi_moe_workspace_size(MI_MOE_NOALLOC_MAX_TOKENS) bytes, about 76 MB at
  * H = 7168, I = 2048, held until the process ends), so num_tokens is at most
  * MI_MOE_NOALLOC_MAX_TOKENS (larger T: MI_MOE_ERR_INVALID, nothing enqueued).
  * The first call on a device looks up that array's address there. The
