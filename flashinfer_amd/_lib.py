@@ -19,7 +19,6 @@ import torch  # noqa: F401  (must precede the CDLL load, see module docstring)
 from . import shapes
 
 HERE = os.path.dirname(os.path.abspath(__file__))
-LIB_PATH = os.path.join(HERE, "libmi_moe.so")  # the default definition
 DEFAULT_SHAPE = shapes.DEFAULT_SHAPE
 DEFAULT = shapes.DEFAULT
 

@@ -163,6 +163,7 @@ __device__ __forceinline__ void store_act(const Plan& p, size_t idx, float v) {
     if (p.act_lo) p.act_lo[idx] = f2bf(v - bf2f(hi));
 }
 
+
 __device__ __forceinline__ int lane_id() { return __lane_id(); }
 
 // Loads 16 bytes through the vector memory path.
@@ -307,14 +308,14 @@ hipError_t launch_gemm2_wide(const Plan& p, const uint8_t* w2, const float* w2s,
 // shapes with 1-, 2-, 4- or 8-wave workgroups and 16/32/64 columns per wave
 // (see the launchers), 10 GEMM2 fused with the combine, 15 "wide" tiles
 // (64 rows for GEMM1, 32 for GEMM2; weights through a per-wave register
-// ring, activations through LDS) for medium row counts, 16 GEMM1 streaming
-// with K split over 4 waves of a workgroup, 17 GEMM2 fused with the combine
+// ring, activations through LDS) for medium row counts, 16 streaming with K
+// split over 4 waves of a workgroup (and, for GEMM2, 9: the same with 64
+// columns per wave), 17 GEMM2 fused with the combine
 // with K split over its 4 waves, 18 the GEMM1 LDS tile of variant 3 with the MFMA
 // operands swapped (one scale factor per lane and tile) and the scale FMAs
 // software-pipelined behind later MFMAs (for GEMM2, the tile of variant 3).
-// An id without a kernel of its own in one GEMM
-// (9, 10 and 17 for GEMM1, 9 and 16 for GEMM2) runs that GEMM's default
-// stream shape.
+// An id without a kernel of its own in one GEMM (9, 10 and 17 for GEMM1)
+// runs that GEMM's default stream shape.
 constexpr int NUM_VARIANTS = 19;
 // GEMM2 variants that also perform the combine (decode sizes only): tiles
 // dealt to the 4 waves, or k-blocks split over them.

@@ -13,10 +13,14 @@
 // the MFMAs idle) the activation is split into bf16 hi + lo, which is wider
 // than the reference's TF32 operand, and the partial rows are fp32.
 //
-// Stream variant (template <MT, D, NW, NQ, MODE>): NW waves per workgroup,
-// each owning NQ 16-column sub-tiles (16 * NQ output columns, inside one
-// 128-column scale block) for 16 * MT slots of one expert; weights go
-// global -> VGPR through a D-deep prefetch ring. MODE (G2_*): the weighted
+// Stream variant (template <MT, D, NW, NQ, MODE, KS>): NW * KS waves per
+// workgroup; wave w owns NQ 16-column sub-tiles (16 * NQ output columns of
+// column group w % NW, inside one 128-column scale block) for 16 * MT slots
+// of one expert, over k-blocks [(w / NW) * IB/KS, +IB/KS); weights go
+// global -> VGPR through a D-deep prefetch ring. With KS > 1 the waves of a
+// column group split K and the first adds the others' partial sums from LDS
+// in split order (deterministic): at decode sizes that puts KS times more
+// waves, and loads, in flight than one wave per column group. MODE (G2_*): the weighted
 // rows go to part (bf16) or part_f32, and with G2_SPLIT the activation is
 // act + act_lo (two bf16 MFMAs per k step against the same bf16 weights).
 //
@@ -66,20 +70,26 @@ __device__ __forceinline__ v4f mfma_block(const Frag16& a, const Frag16& al, con
     return acc;
 }
 
-template <int MT, int D, int NW, int NQ, int MODE>
-__global__ __launch_bounds__(64 * NW) void gemm2_stream_kernel(
+template <int MT, int D, int NW, int NQ, int MODE, int KS>
+__global__ __launch_bounds__(64 * NW * KS) void gemm2_stream_kernel(
     Plan p, const uint8_t* __restrict__ w2, const float* __restrict__ w2s) {
+    constexpr int KB = IB / KS;  // k-blocks per wave
     static_assert(BLK % (16 * NQ) == 0, "a wave's columns stay inside one scale block");
-    static_assert(IB % D == 0, "prefetch depth must divide the k-block count");
+    static_assert(IB % KS == 0 && KB % D == 0, "k split and prefetch depth must divide the k-blocks");
     constexpr bool PREC = MODE == G2_SPLIT;
     constexpr int BM = 16 * MT;
+    // partial sums of waves 1..KS-1 of a column group: [split-1][group][value][lane]
+    __shared__ float red[KS > 1 ? KS - 1 : 1][NW][KS > 1 ? 4 * MT * NQ : 1][64];
     int e, row0, nrows;
     if (!find_tile(p.meta, META_MTILE2, blockIdx.y, BM, e, row0, nrows)) return;
 
     const int tid = threadIdx.x;
     const int lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const int n0 = blockIdx.x * (16 * NQ * NW) + wave * (16 * NQ);
+    const int wc = wave % NW;       // column group
+    const int ks = wave / NW;       // k split
+    const int kb_first = ks * KB;   // first k-block of the wave
+    const int n0 = blockIdx.x * (16 * NQ * NW) + wc * (16 * NQ);
     const int nb = n0 / BLK;  // 128-column scale block of the wave's columns
     const int r = lane & 15, g = lane >> 4;
 
@@ -107,7 +117,7 @@ __global__ __launch_bounds__(64 * NW) void gemm2_stream_kernel(
         for (int q = 0; q < NQ; ++q) acc[i][q] = zero;
 
     auto compute = [&](int d, int kb) __attribute__((always_inline)) {
-        const float sb = sb_ptr[kb];
+        const float sb = sb_ptr[kb_first + kb];
 #pragma unroll
         for (int i = 0; i < MT; ++i) {
 #pragma unroll
@@ -122,18 +132,18 @@ __global__ __launch_bounds__(64 * NW) void gemm2_stream_kernel(
     };
     auto load = [&](int d, int kb) __attribute__((always_inline)) {
 #pragma unroll
-        for (int q = 0; q < NQ; ++q) b[d][q] = ld_frag(b_ptr[q] + kb * BLK);
+        for (int q = 0; q < NQ; ++q) b[d][q] = ld_frag(b_ptr[q] + (kb_first + kb) * BLK);
 #pragma unroll
         for (int i = 0; i < MT; ++i) {
-            a[d][i] = ld_act(a_row[i], kb, g);
-            if constexpr (PREC) al[d][i] = ld_act(al_row[i], kb, g);
+            a[d][i] = ld_act(a_row[i], kb_first + kb, g);
+            if constexpr (PREC) al[d][i] = ld_act(al_row[i], kb_first + kb, g);
         }
     };
 
 #pragma unroll
     for (int d = 0; d < D; ++d) load(d, d);
 #pragma unroll 1
-    for (int kb0 = 0; kb0 < IB - D; kb0 += D) {
+    for (int kb0 = 0; kb0 < KB - D; kb0 += D) {
 #pragma unroll
         for (int d = 0; d < D; ++d) {
             compute(d, kb0 + d);
@@ -149,11 +159,36 @@ __global__ __launch_bounds__(64 * NW) void gemm2_stream_kernel(
 #pragma unroll
         for (int rr = 0; rr < 4; ++rr) wrow[i][rr] = p.sorted_w[row0 + min(i * 16 + g * 4 + rr, nrows - 1)];
 #pragma unroll
-    for (int d = 0; d < D; ++d) compute(d, IB - D + d);
+    for (int d = 0; d < D; ++d) compute(d, KB - D + d);
 #pragma unroll
     for (int i = 0; i < MT; ++i)
 #pragma unroll
         for (int rr = 0; rr < 4; ++rr) asm volatile("" : "+v"(wrow[i][rr]));
+
+    // K split: the other waves of the column group hand their partial sums to
+    // the first through LDS, which adds them in split order.
+    if constexpr (KS > 1) {
+        if (ks > 0) {
+#pragma unroll
+            for (int i = 0; i < MT; ++i)
+#pragma unroll
+                for (int q = 0; q < NQ; ++q)
+#pragma unroll
+                    for (int rr = 0; rr < 4; ++rr)
+                        red[ks - 1][wc][(i * NQ + q) * 4 + rr][lane] = acc[i][q][rr];
+        }
+        __syncthreads();
+        if (ks > 0) return;
+#pragma unroll
+        for (int k = 0; k < KS - 1; ++k)
+#pragma unroll
+            for (int i = 0; i < MT; ++i)
+#pragma unroll
+                for (int q = 0; q < NQ; ++q)
+#pragma unroll
+                    for (int rr = 0; rr < 4; ++rr)
+                        acc[i][q][rr] += red[k][wc][(i * NQ + q) * 4 + rr][lane];
+    }
 
     // Epilogue: weight each slot's row by its routing weight (kernel.py:364)
     // and store it (bf16, or fp32 unless G2_BF16) for the combine.
@@ -190,23 +225,25 @@ int gemm2_bm(int variant) {
     }
 }
 
-template <int MT, int D, int NW, int NQ>
+template <int MT, int D, int NW, int NQ, int KS = 1>
 static void launch_stream2(const Plan& p, const uint8_t* w2, const float* w2s, hipStream_t s) {
-    // a ring deeper than the shape's k-blocks allow falls back to 2 deep
-    constexpr int DD = IB % D == 0 ? D : 2;
+    // a ring deeper than the shape's k-blocks allow falls back to 2 deep (or 1)
+    constexpr int KB = IB / KS;
+    constexpr int DD = KB % D == 0 ? D : (KB % 2 == 0 ? 2 : 1);
     dim3 grid(H / (16 * NQ * NW), max_mtiles(p.T, 16 * MT));
+    const dim3 block(64 * NW * KS);
     switch (gemm2_mode(p)) {
         case G2_SPLIT:
-            hipLaunchKernelGGL((gemm2_stream_kernel<MT, DD, NW, NQ, G2_SPLIT>), grid, dim3(64 * NW), 0, s,
-                               p, w2, w2s);
+            hipLaunchKernelGGL((gemm2_stream_kernel<MT, DD, NW, NQ, G2_SPLIT, KS>), grid, block, 0, s, p,
+                               w2, w2s);
             break;
         case G2_F32:
-            hipLaunchKernelGGL((gemm2_stream_kernel<MT, DD, NW, NQ, G2_F32>), grid, dim3(64 * NW), 0, s,
-                               p, w2, w2s);
+            hipLaunchKernelGGL((gemm2_stream_kernel<MT, DD, NW, NQ, G2_F32, KS>), grid, block, 0, s, p,
+                               w2, w2s);
             break;
         default:
-            hipLaunchKernelGGL((gemm2_stream_kernel<MT, DD, NW, NQ, G2_BF16>), grid, dim3(64 * NW), 0, s,
-                               p, w2, w2s);
+            hipLaunchKernelGGL((gemm2_stream_kernel<MT, DD, NW, NQ, G2_BF16, KS>), grid, block, 0, s, p,
+                               w2, w2s);
     }
 }
 
@@ -223,10 +260,12 @@ hipError_t launch_gemm2(const Plan& p, const uint8_t* w2, const float* w2s, int 
         case 6: launch_stream2<1, 4, 1, 1>(p, w2, w2s, s); break;
         case 7: launch_stream2<2, 4, 1, 2>(p, w2, w2s, s); break;
         case 8: launch_stream2<1, 8, 4, 2>(p, w2, w2s, s); break;
+        case 9: launch_stream2<1, 2, 1, 4, 4>(p, w2, w2s, s); break;
         case 11: launch_stream2<1, 8, 1, 1>(p, w2, w2s, s); break;
         case 12: launch_stream2<2, 4, 1, 1>(p, w2, w2s, s); break;
         case 13: launch_stream2<1, 4, 1, 4>(p, w2, w2s, s); break;
         case 14: launch_stream2<1, 2, 1, 4>(p, w2, w2s, s); break;
+        case 16: launch_stream2<1, 4, 1, 2, 4>(p, w2, w2s, s); break;
         default: launch_stream2<1, 2, 1, 2>(p, w2, w2s, s); break;
     }
     return hipGetLastError();
