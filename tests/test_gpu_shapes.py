@@ -39,9 +39,10 @@ def test_library_reports_its_shape():
 
 
 # default kernels by T: fused front end, one-wave / workgroup / chunked sort,
-# K-split stream, wide and LDS-tiled GEMMs
-@pytest.mark.parametrize("T,offset", [(1, 0), (4, 32), (16, 0), (64, 96), (200, 0), (512, 224),
-                                      (1024, 64), (2049, 0)])
+# K-split stream (up to T = 256 at this shape, with a sort launch above 64),
+# wide and LDS-tiled GEMMs
+@pytest.mark.parametrize("T,offset", [(1, 0), (4, 32), (16, 0), (64, 96), (65, 0), (200, 0),
+                                      (256, 160), (257, 0), (512, 224), (1024, 64), (2049, 0)])
 def test_default_kernels_second_shape(T, offset):
     log(f"test_default_kernels_second_shape[T={T}]")
     wl = _wl(T, 500 + T, offset)
