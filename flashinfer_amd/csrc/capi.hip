@@ -8,6 +8,7 @@
 // (the reference syncs three times, kernel.py:572, :718, :773). Routing and
 // the sort fold into GEMM1 at T = 1, the sort alone up to T = 256 (the
 // stream GEMM1 kernels up to 64, the wide one above); see pick_front.
+#include <dlfcn.h>
 #include <math.h>
 #include <stdarg.h>
 #include <stdio.h>
@@ -147,6 +148,35 @@ Plan make_plan(void* workspace, const mi_moe_layout& L, int64_t T, int64_t local
     p.part_f32 = nullptr;
     p.act_lo = nullptr;
     return p;
+}
+
+// Named ranges for profilers, as the reference's _profile_region gives its
+// phases (kernel.py:10-24, :678-823): with FIB_PROFILE_PHASES=1 in the
+// environment at the first call, each phase's launches sit in a roctx range
+// named as the reference names that phase (route + sort ->
+// phase1_route_permute, GEMM1 with its SwiGLU -> phase3_gemm1, phase5_gemm2,
+// the combine with its bf16 cast -> phase6_scatter), inside an "mi_moe_run"
+// range, so `rocprofv3 --marker-trace` attributes the kernels. The roctx
+// library is looked up at run time, so the operator does not link against it.
+struct Roctx {
+    int (*push)(const char*);
+    int (*pop)();
+};
+
+const Roctx* roctx() {
+    static const Roctx r = [] {
+        Roctx x{nullptr, nullptr};
+        const char* f = getenv("FIB_PROFILE_PHASES");
+        if (!f || f[0] != '1' || f[1] != 0) return x;
+        void* h = dlopen("librocprofiler-sdk-roctx.so.1", RTLD_NOW | RTLD_LOCAL);
+        if (!h) h = dlopen("libroctx64.so.4", RTLD_NOW | RTLD_LOCAL);
+        if (!h) return x;
+        x.push = reinterpret_cast<int (*)(const char*)>(dlsym(h, "roctxRangePushA"));
+        x.pop = reinterpret_cast<int (*)()>(dlsym(h, "roctxRangePop"));
+        if (!x.push || !x.pop) x = Roctx{nullptr, nullptr};
+        return x;
+    }();
+    return r.push ? &r : nullptr;
 }
 
 // GEMM variants by token count. MI_MOE_VARIANT="v" or "v1,v2" overrides
@@ -423,8 +453,20 @@ static int run_impl(const mi_moe_args* a, hipStream_t s, hipEvent_t const* ev,
     if (g2_mode != G2_BF16) p.part_f32 = (float*)p.part;
     if (g2_mode == G2_SPLIT) p.act_lo = (uint16_t*)((uint8_t*)a->workspace + L.act_lo);
     hipError_t err = hipSuccess;
+    // mark(i) opens phase i (0 route, 1 sort, 2 GEMM1, 3 GEMM2, 4 combine)
+    // and closes phase i - 1; the named ranges join route and sort.
+    const Roctx* rx = roctx();
     auto mark = [&](int i) {
         if (ev && err == hipSuccess) err = hipEventRecord(ev[i], s);
+        if (!rx) return;
+        switch (i) {
+            case 0: rx->push("mi_moe_run"); rx->push("phase1_route_permute"); break;
+            case 2: rx->pop(); rx->push("phase3_gemm1"); break;
+            case 3: rx->pop(); rx->push("phase5_gemm2"); break;
+            case 4: rx->pop(); rx->push("phase6_scatter"); break;
+            case 5: rx->pop(); rx->pop(); break;
+            default: break;
+        }
     };
     const int bias_f32 = a->bias_dtype == MI_MOE_DTYPE_F32;
     Front front = pick_front(T, var.g1);

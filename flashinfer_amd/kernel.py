@@ -201,8 +201,14 @@ def run(
     args = (routing_logits, routing_bias, hidden_states, hidden_states_scale, gemm1_weights,
             gemm1_weights_scale, gemm2_weights, gemm2_weights_scale, local_expert_offset,
             routed_scaling_factor, output)
-    if _phase_timing_enabled() and isinstance(output, torch.Tensor) and output.is_cuda:
-        _emit_phase_timing(args, int(routing_logits.shape[0]))
+    if os.environ.get("FIB_PROFILE_PHASES") == "1":
+        # the reference's profiler regions (kernel.py:10-24): a record_function
+        # range for torch.profiler here; the library adds roctx ranges per phase
+        with torch.autograd.profiler.record_function("mi_moe_run"):
+            if _phase_timing_enabled() and isinstance(output, torch.Tensor) and output.is_cuda:
+                _emit_phase_timing(args, int(routing_logits.shape[0]))
+            else:
+                _call(*args, None)
         return None
     _call(*args, None)
     return None

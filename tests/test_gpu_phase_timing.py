@@ -40,3 +40,20 @@ def test_phase_timing_json_written_once(tmp_path, monkeypatch):
     out_path.unlink()
     run_gpu(wl)
     assert not out_path.exists()
+
+
+def test_profiler_range(monkeypatch):
+    """With FIB_PROFILE_PHASES=1 each call sits in a record_function range
+    (the reference's _profile_region, kernel.py:10-24) that torch.profiler
+    sees; without it there is none. The output is unchanged."""
+    log("test_profiler_range")
+    wl = W.standard("c1_t16")
+    plain = run_gpu(wl)
+    monkeypatch.delenv("FIB_PHASE_TIMING_OUTPUT", raising=False)
+    for flag, expect in (("1", True), ("0", False)):
+        monkeypatch.setenv("FIB_PROFILE_PHASES", flag)
+        with torch.profiler.profile(activities=[torch.profiler.ProfilerActivity.CPU]) as prof:
+            out = run_gpu(wl)
+        names = {e.key for e in prof.key_averages()}
+        assert ("mi_moe_run" in names) == expect, sorted(names)[:20]
+        assert torch.equal(out.view(torch.int16), plain.view(torch.int16))
