@@ -145,25 +145,35 @@ __global__ __launch_bounds__(1024) void sort_count_kernel(Plan p) {
 // places its tokens.
 __global__ __launch_bounds__(1024) void sort_place_kernel(Plan p, int nchunks, int bm1, int bm2) {
     __shared__ int base[EL];
+    __shared__ int s_before[EL], s_total[EL];
     __shared__ int wcnt[CHUNK / 64][EL];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int cb = blockIdx.x;
-    if (wave == 0) {
-        int before = 0, total = 0;
-        if (lane < EL) {
-            for (int c = 0; c < nchunks; ++c) {
-                const int v = p.chunk_cnt[c * EL + lane];
-                before += c < cb ? v : 0;
-                total += v;
-            }
-        }
-        const int off = scan_counts(p, lane, total, bm1, bm2, cb == 0);
-        if (lane < EL) base[lane] = off + before;
-    }
-    __syncthreads();
+    // The chunk's top-k rows are loaded first, so their round trip overlaps
+    // the chunk totals'.
     const int t = cb * CHUNK + tid;
     const bool valid = t < p.T;
     const TokLocal tl = load_local(p.topk_ids, p.topk_w, t, valid, p.local_offset);
+    // Chunk totals, every (chunk, expert) count loaded by its own thread (one
+    // round trip, not one per chunk) and summed with LDS integer atomics
+    // (exact, so the order does not matter).
+    if (tid < EL) { s_before[tid] = 0; s_total[tid] = 0; }
+    __syncthreads();
+    for (int i = tid; i < nchunks * EL; i += CHUNK) {
+        const int v = p.chunk_cnt[i];
+        const int c = i / EL, e = i % EL;
+        if (v) {
+            atomicAdd(&s_total[e], v);
+            if (c < cb) atomicAdd(&s_before[e], v);
+        }
+    }
+    __syncthreads();
+    if (wave == 0) {
+        const int total = lane < EL ? s_total[lane] : 0;
+        const int off = scan_counts(p, lane, total, bm1, bm2, cb == 0);
+        if (lane < EL) base[lane] = off + s_before[lane];
+    }
+    __syncthreads();
     place_chunk(p, t, valid, tl, base, wcnt, tid, lane, wave);
 }
 
