@@ -237,12 +237,15 @@ Front pick_front(int64_t T, int g1) {
 }
 
 // Layers smaller than 7168 x 2048 keep the stream kernels (K-split GEMM1,
-// 64-column GEMM2 waves) up to T = 256. Measured at H = 4096, I = 1536 per
-// call: T = 80 104.2 against 127.5 us with the wide GEMM1, T = 160 104.0
-// against 123.5, T = 256 113.9 against 130.1 (wide GEMM2), T = 384 153.0
-// against 140.5 (the wide GEMM1 wins again); at 7168 x 2048 the wide
-// kernels lead from T = 96.
-constexpr bool kStreamTo256 = (int64_t)H * I < (int64_t)7168 * 2048;
+// 64-column GEMM2 waves) while T * top_k <= 8 * global experts (about 8 slots
+// per local expert), at 7168 x 2048 only to T = 64 (about 2). Measured per
+// call at H = 4096, I = 1536 with 32 of 256 experts, top-8: T = 80 104.2
+// against 127.5 us with the wide GEMM1, T = 160 104.0 against 123.5, T = 256
+// 113.9 against 130.1, T = 384 153.0 against 140.5 (the wide kernels win);
+// with 16 of 128 experts, top-6: T = 128 54.3 against 61.8, T = 256 88.6
+// against 74.9 (wide); at 7168 x 2048 the wide kernels lead from T = 96.
+constexpr bool kSmallLayer = (int64_t)H * I < (int64_t)7168 * 2048;
+constexpr int64_t kStreamMaxSlotsPerExpert = 8;
 
 Variants pick_variants(int64_t T) {
     Variants v;
@@ -256,7 +259,7 @@ Variants pick_variants(int64_t T) {
     else if (T <= 4) v = {16, VARIANT_GEMM2_COMBINE_KS};
     else if (T <= 8) v = {16, 5};
     else if (T <= 64) v = {16, 14};
-    else if (kStreamTo256 && T <= 256) v = {16, 14};
+    else if (kSmallLayer && T * TOPK <= kStreamMaxSlotsPerExpert * EG) v = {16, 14};
     else if (T <= 128) v = {15, 14};  // the wide GEMM1 folds in the sort from T = 65
     else if (T <= 176) v = {15, 13};  // wide GEMM2 ahead by 3.5 us at T = 192, behind by ~2 at 160
     else if (T <= 256) v = {15, 15};

@@ -9,8 +9,8 @@ The reference's routing kernel takes these as constexpr parameters
 (kernel.py:371-389); here each is a library build. Bars, as for the default
 definition: routing sets bit-exact (and the same order), weights within 1e-6;
 sort tables bit-exact; output |out-ref| <= 1e-2*|ref| + 1e-2*max|ref| against
-the oracle run with the definition's parameters, at T = 1, 64, 1024, 8192 and
-a skewed batch.
+the oracle run with the definition's parameters, at T = 1, 64, 170, 171, 1024,
+8192 and a skewed batch.
 """
 import pytest
 import torch
@@ -95,7 +95,9 @@ def _check_output(wl, out, tokens):
     assert rep["n_bad"] == 0, rep
 
 
-@pytest.mark.parametrize("T", [1, 64, 1024, 8192])
+# 170 / 171: the 128-expert top-6 build's switch from the stream to the wide
+# kernels (T * top_k <= 8 * global experts)
+@pytest.mark.parametrize("T", [1, 64, 170, 171, 1024, 8192])
 @pytest.mark.parametrize("defn", DEFS, ids=lambda d: d.tag)
 def test_definition_parity(defn, T):
     log(f"test_definition_parity[{defn.name}-T={T}]")
