@@ -2,7 +2,8 @@
 definition: H=7168, I=2048, 32 of 256 experts, 8 groups, top-4 groups,
 top-8), one libmi_moe_<tag>.so per further definition in
 shapes.DEFINITIONS, and libmi_peaks.so (achievable-peak probes used by
-bench.py), for gfx950 with hipcc.
+bench.py), for gfx950 with hipcc; and _mi_moe_host, the native host path of
+kernel.run (host C++ against torch's headers, built with g++).
 
 Usage: python -m flashinfer_amd.build [--jobs N] [--save-temps]
 The shared libraries land next to this file so they travel with the tree.
@@ -14,6 +15,7 @@ import os
 import shutil
 import subprocess
 import sys
+import sysconfig
 from concurrent.futures import ThreadPoolExecutor
 
 from .shapes import DEFINITIONS, lib_name_of
@@ -85,6 +87,34 @@ def _link(objs, out):
     os.replace(tmp, out)
 
 
+HOST_SRC = os.path.join(CSRC, "host_bind.cpp")
+HOST_LIB = os.path.join(HERE, "_mi_moe_host" + sysconfig.get_config_var("EXT_SUFFIX"))
+
+
+def build_host() -> str:
+    """The torch extension _mi_moe_host: host code only, so g++ builds it
+    (against torch's headers and its bundled pybind11) without hipcc."""
+    import torch
+    tdir = os.path.dirname(torch.__file__)
+    tlib = os.path.join(tdir, "lib")
+    rocm = os.environ.get("ROCM_PATH", "/opt/rocm")
+    abi = int(torch._C._GLIBCXX_USE_CXX11_ABI)
+    tmp = HOST_LIB + ".tmp"
+    cmd = [shutil.which("g++") or "g++", "-O2", "-shared", "-fPIC", "-std=c++17", "-Wall",
+           f"-D_GLIBCXX_USE_CXX11_ABI={abi}", "-DUSE_ROCM", "-D__HIP_PLATFORM_AMD__=1",
+           "-I", os.path.join(tdir, "include"),
+           "-I", os.path.join(tdir, "include", "torch", "csrc", "api", "include"),
+           "-I", sysconfig.get_paths()["include"], "-I", os.path.join(rocm, "include"),
+           HOST_SRC, "-o", tmp, "-L", tlib, "-lc10", "-lc10_hip", "-ltorch", "-ltorch_cpu",
+           "-ltorch_python", "-L", os.path.join(rocm, "lib"), "-lamdhip64",
+           f"-Wl,-rpath,{tlib}"]
+    r = subprocess.run(cmd, capture_output=True, text=True)
+    if r.returncode != 0:
+        raise RuntimeError(f"g++ failed on host_bind.cpp:\n{r.stderr}")
+    os.replace(tmp, HOST_LIB)
+    return HOST_LIB
+
+
 def build(jobs: int = 8, extra=()) -> str:
     os.makedirs(BUILD, exist_ok=True)
     jobs_list = [(s, d) for d in DEFINITIONS for s in SOURCES] + [(s, None) for s in PEAKS_SOURCES]
@@ -94,6 +124,7 @@ def build(jobs: int = 8, extra=()) -> str:
     for k, d in enumerate(DEFINITIONS):
         _link(objs[k * n:(k + 1) * n], os.path.join(HERE, lib_name_of(d)))
     _link(objs[len(DEFINITIONS) * n:], PEAKS_LIB)
+    build_host()
     return LIB
 
 

@@ -58,11 +58,38 @@ def _capturing() -> bool:
     return torch.cuda.is_current_stream_capturing()
 
 
+# The native host path (host_bind.cpp): checks, workspace and argument block
+# of the plain call in C++, one Python-to-C++ call; it also holds the workspace
+# cache, so both paths share one workspace per (thread, device, stream).
+try:
+    from . import _mi_moe_host as _HOST
+except ImportError:
+    _HOST = None
+_NOT_FAST = -1 if _HOST is None else _HOST.NOT_FAST
+_HOST_REGISTERED: set = set()
+
+
+def host_path_loaded() -> bool:
+    """Whether the native host path (_mi_moe_host) is in use."""
+    return _HOST is not None
+
+
+def _register_host(defn, L) -> None:
+    """Lets the native host path call ``defn``'s library for its shapes."""
+    if _HOST is not None and defn not in _HOST_REGISTERED:
+        _HOST.register_definition(defn.EL, 2 * defn.I, defn.H, defn.EG,
+                                  ctypes.cast(L.mi_moe_run, ctypes.c_void_p).value,
+                                  ctypes.cast(L.mi_moe_workspace_size, ctypes.c_void_p).value)
+        _HOST_REGISTERED.add(defn)
+
+
 def _workspace(device: torch.device, stream: int, nbytes: int) -> torch.Tensor:
     if _capturing():
         ws = torch.empty(max(nbytes, 256), dtype=torch.uint8, device=device)
         _CAPTURED.append(ws)
         return ws
+    if _HOST is not None:
+        return _HOST.workspace(device.index, stream, nbytes)
     key = (device.index, stream)
     _workspaces = _workspace_cache()
     ws = _workspaces.get(key)
@@ -198,6 +225,15 @@ def run(
     routed_scaling_factor: float,
     output: torch.Tensor,
 ):
+    if _HOST is not None:
+        # plain case in C++; anything else (errors included) on the general path
+        st = _HOST.run(routing_logits, routing_bias, hidden_states, hidden_states_scale,
+                       gemm1_weights, gemm1_weights_scale, gemm2_weights, gemm2_weights_scale,
+                       local_expert_offset, routed_scaling_factor, output)
+        if st == 0:
+            return None
+        if st != _NOT_FAST:
+            _lib.check(st, _lib.lib(_definition_of(routing_logits, gemm1_weights)))
     args = (routing_logits, routing_bias, hidden_states, hidden_states_scale, gemm1_weights,
             gemm1_weights_scale, gemm2_weights, gemm2_weights_scale, local_expert_offset,
             routed_scaling_factor, output)
@@ -365,6 +401,7 @@ def _call(routing_logits, routing_bias, hidden_states, hidden_states_scale, gemm
 def _issue(defn, T, device, stream, cur, ins, out, offset, rsf, events, hidden_bf16):
     """Fills the argument block and calls the library on `stream`."""
     L = _lib.lib(defn)
+    _register_host(defn, L)
     need = _ws_size(T, defn)
     ws = _workspace(device, stream, need)
     args = _lib.MiMoeArgs(
@@ -511,4 +548,9 @@ def last_workspace(device: torch.device | None = None) -> torch.Tensor:
     parity checks)."""
     device = device or torch.device("cuda", torch.cuda.current_device())
     stream = torch.cuda.current_stream(device).cuda_stream
+    if _HOST is not None:
+        ws = _HOST.cached_workspace(device.index, stream)
+        if ws is None:
+            raise KeyError((device.index, stream))
+        return ws
     return _workspace_cache()[(device.index, stream)]

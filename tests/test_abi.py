@@ -297,3 +297,35 @@ def test_run_noalloc_rejects_before_launch():
     a = _args(workspace=None, workspace_bytes=0, num_tokens=_lib.MI_MOE_NOALLOC_MAX_TOKENS + 1)
     assert L.mi_moe_run_noalloc(ctypes.byref(a), None) == _lib.MI_MOE_ERR_INVALID
     assert b"MI_MOE_NOALLOC_MAX_TOKENS" in L.mi_moe_last_error()
+
+
+def test_native_host_path_module():
+    """The native host path is built and loaded, and leaves every case it does
+    not handle (here: tensors not on a GPU) to the general path."""
+    assert kernel.host_path_loaded()
+    H = kernel._HOST
+    for name in ("run", "register_definition", "workspace", "cached_workspace"):
+        assert callable(getattr(H, name)), name
+    assert H.NOT_FAST == -1
+    T = 2
+    args = [torch.zeros(T, 256), torch.zeros(256, dtype=torch.bfloat16),
+            torch.zeros(T, 7168).to(torch.float8_e4m3fn), torch.zeros(56, T),
+            torch.empty(32, 4096, 7168, dtype=torch.float8_e4m3fn), torch.zeros(32, 32, 56),
+            torch.empty(32, 7168, 2048, dtype=torch.float8_e4m3fn), torch.zeros(32, 56, 16),
+            0, 2.5, torch.zeros(T, 7168, dtype=torch.bfloat16)]
+    assert H.run(*args) == H.NOT_FAST
+    assert H.run(*(["not a tensor"] * 8 + [0, 2.5, "x"])) == H.NOT_FAST
+
+
+def test_native_host_registration():
+    """Registering a definition's library twice is a no-op; another library
+    for the same shapes is refused."""
+    L = _lib.lib()
+    kernel._register_host(_lib.DEFAULT, L)
+    kernel._register_host(_lib.DEFAULT, L)
+    d = _lib.DEFAULT
+    run_addr = ctypes.cast(L.mi_moe_run, ctypes.c_void_p).value
+    size_addr = ctypes.cast(L.mi_moe_workspace_size, ctypes.c_void_p).value
+    kernel._HOST.register_definition(d.EL, 2 * d.I, d.H, d.EG, run_addr, size_addr)
+    with pytest.raises(RuntimeError, match="another library"):
+        kernel._HOST.register_definition(d.EL, 2 * d.I, d.H, d.EG, size_addr, size_addr)
