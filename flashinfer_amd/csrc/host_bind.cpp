@@ -228,6 +228,9 @@ int run(py::handle logits_h, py::handle bias_h, py::handle hs_h, py::handle hss_
     a.reserved = 0;
     a.workspace = ws.data_ptr();
     a.workspace_bytes = (size_t)ws.numel();
+    // The launches run without the GIL (as a ctypes call would); the caller's
+    // frame keeps every tensor alive until this returns.
+    py::gil_scoped_release nogil;
     return d->run(&a, stream);
 }
 
