@@ -8,7 +8,7 @@ import torch
 
 from _helpers import gpu_args, log
 
-from flashinfer_amd import _lib, kernel
+from flashinfer_amd import _lib, kernel, shapes
 from flashinfer_amd import workloads as W
 
 pytestmark = pytest.mark.gpu
@@ -120,3 +120,25 @@ def test_native_path_reports_library_errors():
     assert kernel._HOST.run(*a, out) not in (0, kernel._NOT_FAST)
     with pytest.raises(_lib.MiMoeError, match="aligned"):
         kernel.run(*a, out)
+
+
+@pytest.mark.parametrize("defn", [d for d in shapes.DEFINITIONS if d != shapes.DEFAULT],
+                         ids=lambda d: d.tag)
+def test_native_path_other_definitions_and_fp32_bias(defn, monkeypatch):
+    """Each definition's library is registered for its own shapes; fp32
+    routing bias takes the native path too; outputs equal the Python path's."""
+    log(f"test_native_path_other_definitions_and_fp32_bias[{defn.tag}]")
+    wl = W.make_for(defn, f"{defn.tag}_host", 24, 7300, local_expert_offset=0)
+    args = gpu_args(wl)
+    args[1] = args[1].float()
+    ref = _outputs(args, wl.T, defn.H)
+    with monkeypatch.context() as m:
+        m.setattr(kernel, "_HOST", None)
+        kernel.run(*args, ref)
+    kernel.run(*args, _outputs(args, wl.T, defn.H))  # registers the definition
+    out = _outputs(args, wl.T, defn.H)
+    with monkeypatch.context() as m:
+        m.setattr(kernel, "_call", _general_only)
+        kernel.run(*args, out)
+    torch.cuda.synchronize()
+    assert torch.equal(out.view(torch.int16), ref.view(torch.int16))
