@@ -141,7 +141,16 @@ def device_args(wl, dev):
         wl.local_expert_offset, wl.routed_scaling_factor]
 
 
-def time_workload(wl, steps, warmup, trials=5):
+WARM_S = 0.05         # untimed calls after the warmup count, so clocks have ramped up
+MIN_TRIAL_US = 4000.0  # sweep entries: calls per trial raised to fill at least this
+
+
+def time_workload(wl, steps, warmup, trials=5, exact=True):
+    """Times ``steps`` calls per trial (exact=True, the headline), or for a
+    sweep entry enough calls that a trial lasts MIN_TRIAL_US, after
+    ``warmup`` calls and then WARM_S of untimed calls (a 20-call trial of a
+    40 us call would otherwise run partly at the clocks of the idle GPU
+    that preceded it: ~10 % slower at T = 4 and 16)."""
     from flashinfer_amd import _lib, kernel
     dev = torch.device("cuda", 0)
     args = device_args(wl, dev)
@@ -149,16 +158,24 @@ def time_workload(wl, steps, warmup, trials=5):
     for _ in range(warmup):
         kernel.run(*args, out)
     torch.cuda.synchronize()
+    n_warm, t0 = 0, time.perf_counter()
+    while time.perf_counter() - t0 < WARM_S:
+        for _ in range(10):
+            kernel.run(*args, out)
+        torch.cuda.synchronize()
+        n_warm += 10
+    est_us = (time.perf_counter() - t0) * 1e6 / n_warm
+    calls = steps if exact else max(steps, int(MIN_TRIAL_US / est_us) + 1)
     S, A_e, max_rows = routing_stats(wl.T)
-    # value: plain calls, trials x steps, bracketed by synchronize
+    # value: plain calls, trials x calls, bracketed by synchronize
     trial_us = []
     for tr in range(trials):
         torch.cuda.synchronize()
         t0 = time.perf_counter()
-        for k in range(steps):
+        for k in range(calls):
             kernel.run(*args, out)
         torch.cuda.synchronize()
-        trial_us.append((time.perf_counter() - t0) * 1e6 / steps)
+        trial_us.append((time.perf_counter() - t0) * 1e6 / calls)
     # per-kernel durations: the same calls with HIP events recorded between the
     # kernels on their stream (the records add a little time between kernels)
     nev = _lib.NUM_PHASES + 1
@@ -177,7 +194,7 @@ def time_workload(wl, steps, warmup, trials=5):
                 phase_sum[p] += ev[k][p].elapsed_time(ev[k][p + 1]) * 1e3
     phase_us = [s / (steps * trials) for s in phase_sum]
     cold_us = time_cold(args, out, min(steps, 20))
-    graph_us = time_graph(args, out, steps)
+    graph_us = time_graph(args, out, calls)
     us = statistics.median(trial_us)
     B = call_bytes(wl.T, A_e)
     F1, F2 = S * GEMM1_FLOPS_PER_SLOT, S * GEMM2_FLOPS_PER_SLOT
@@ -191,6 +208,7 @@ def time_workload(wl, steps, warmup, trials=5):
         "workload": wl.name, "T": wl.T, "local_expert_offset": wl.local_expert_offset,
         "slots": S, "active_experts": A_e, "max_rows_per_expert": max_rows,
         "us_per_call": round(us, 2), "trials_us": [round(x, 2) for x in trial_us],
+        "calls_per_trial": calls,
         "us_per_call_with_phase_events": round(statistics.median(prof_us), 2),
         "gbps": round(B / t / 1e9, 1), "tflops": round(F / t / 1e12, 2),
         "hbm_frac": round(B / t / 1e9 / HBM_PEAK_GBS, 4),
@@ -570,7 +588,7 @@ def main():
                 continue
             w = make(name)
             steps = a.steps if w.T <= 1024 else max(10, a.steps // 2)
-            r = time_workload(w, steps, a.warmup)
+            r = time_workload(w, steps, a.warmup, exact=False)
             log(f"[bench] {json.dumps(r)}")
             sweep.append(r)
             del w

@@ -254,10 +254,17 @@ Variants pick_variants(int64_t T) {
     // wide kernels (register-ring weights, LDS activations) for roughly 5 to
     // 70 rows per expert (GEMM2 from ~10 to ~15), the LDS-tiled kernels beyond.
     // GEMM2 with the combine (K split over its 4 waves, which keeps them all
-    // busy with fewer than 4 row tiles): one launch fewer where launches dominate
-    if (T <= 1) v = {5, VARIANT_GEMM2_COMBINE_KS};
-    else if (T <= 4) v = {16, VARIANT_GEMM2_COMBINE_KS};
-    else if (T <= 8) v = {16, 5};
+    // busy with fewer than 4 row tiles): one launch fewer where launches
+    // dominate (T <= 4). From T = 1 on the K-split GEMM1 (per call with two
+    // local slots: 27.9 against 35.6 us for single-wave workgroups, 0.4 us
+    // slower with none); at 7168 x 2048 the K-split 32-column GEMM2 waves up
+    // to T = 16: with random routing T = 12 30.8 against 37.0 us for 64-column
+    // waves, T = 16 77.1 against 79.3; with every token on the same 8 experts
+    // (16 activation rows per tile, which 32-column waves re-read twice as
+    // often) T = 16 83.9 against 77.0, T = 32 158.6 against 139.0.
+    if (T <= 4) v = {16, VARIANT_GEMM2_COMBINE_KS};
+    else if (T <= 8 && kSmallLayer) v = {16, 5};
+    else if (T <= 16 && !kSmallLayer) v = {16, 16};
     else if (T <= 64) v = {16, 14};
     else if (kSmallLayer && T * TOPK <= kStreamMaxSlotsPerExpert * EG) v = {16, 14};
     else if (T <= 128) v = {15, 14};  // the wide GEMM1 folds in the sort from T = 65

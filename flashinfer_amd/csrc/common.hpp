@@ -169,9 +169,80 @@ __device__ __forceinline__ int lane_id() { return __lane_id(); }
 // Loads 16 bytes through the vector memory path.
 __device__ __forceinline__ v4i ld16(const void* p) { return *reinterpret_cast<const v4i*>(p); }
 
-__device__ __forceinline__ v8i ld_frag(const uint8_t* p) {
+// Weight operand of one 16-row x 128-byte k-block, read as whole lines.
+// Lane l (n = l % 16, q = l / 16) loads 16 bytes at wl_off from row n % 8
+// (x) and from row 8 + n % 8 (y), bytes [32q + 16(n / 8), +16): each load
+// instruction covers 8 complete 128-byte lines, which non-temporal loads
+// stream from HBM about 15% faster than the 16 half lines of a row-per-lane
+// layout (measured on MI355X: 7.1 against 6.2 TB/s plain, and 5.7 TB/s for
+// half lines with the non-temporal hint). Rotating each 16-lane row by 8
+// (DPP; lanes 8-15 take y of lane n - 8, lanes 0-7 x of lane n + 8) leaves
+// lane l with row n, bytes [32q, 32q + 32): the MFMA operand in its own k
+// order, which the activation side reads with ld_afrag (fp8) or as 32
+// consecutive bf16.
+__device__ __forceinline__ size_t wl_off(int lane, size_t row_stride) {
+    return (size_t)(lane & 7) * row_stride + (lane >> 4) * 32 + ((lane >> 3) & 1) * 16;
+}
+
+// Buffer resource over `bytes` bytes at a uniform `base`: raw buffer loads
+// through it are range-checked (an offset past the end reads 0) and carry
+// their cache policy as an immediate.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t wrsrc(const void* base, uint32_t bytes) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, (int)bytes, 0x00020000);
+}
+
+// The two loads of a weight k-block (off = row base + wl_off, stride8 = 8
+// rows), kept raw in a prefetch ring: the exchange (wl_frag) runs where the
+// operand is consumed, so the loads stay in flight until then.
+// NT: non-temporal loads. They stream weights that no other row tile of the
+// launch reads again ~12 % faster; where several row tiles of an expert
+// re-read its weights, plain loads keep them in L2 / MALL for the others
+// (with the hint each tile fetched them from HBM again: T=1024 with up to 8
+// row tiles per expert, GEMM1 564 against 475 us). The policy is a template
+// argument picked per launch from T (wt_nt): chosen per workgroup at run
+// time, the two load forms in one loop cost the stream GEMM1 its registers
+// (spills).
+struct WRaw {
+    v4i x, y;
+};
+template <bool NT>
+__device__ __forceinline__ WRaw ld_wraw(__amdgpu_buffer_rsrc_t r, uint32_t off, uint32_t stride8) {
+    constexpr int AUX = NT ? 2 : 0;  // cache policy: nt
+    WRaw w;
+    w.x = __builtin_bit_cast(v4i, __builtin_amdgcn_raw_buffer_load_b128(r, (int)off, 0, AUX));
+    w.y = __builtin_bit_cast(v4i, __builtin_amdgcn_raw_buffer_load_b128(r, (int)(off + stride8), 0, AUX));
+    return w;
+}
+
+// Weight load policy of a launch with T tokens and `bm`-row tiles: non-
+// temporal while an expert holds about one row tile or less on average
+// (T * top_k <= bm * global experts / 4: T <= 128 for 16-row tiles, 512 for
+// 64-row tiles with the default routing; a shard's experts can hold twice
+// the uniform share, as at T = 1024 offset 0). Measured per GEMM with random
+// routing at T = 16 / 64 / 100 / 256 / 512: 9-12 % faster with the hint;
+// with every token on the same 8 experts (T = 64 / 256: 4 row tiles each)
+// 5-7 % slower, the price of not knowing the counts on the host.
+inline bool wt_nt(int64_t T, int bm) { return T * TOPK <= (int64_t)bm * EG / 4; }
+
+__device__ __forceinline__ v8i wl_frag(const WRaw& w) {
+    constexpr int ROR8 = 0x128;  // DPP row_ror:8
+    v8i r;
+    r.s0 = __builtin_amdgcn_update_dpp(w.x.x, w.y.x, ROR8, 0xF, 0xC, false);
+    r.s1 = __builtin_amdgcn_update_dpp(w.x.y, w.y.y, ROR8, 0xF, 0xC, false);
+    r.s2 = __builtin_amdgcn_update_dpp(w.x.z, w.y.z, ROR8, 0xF, 0xC, false);
+    r.s3 = __builtin_amdgcn_update_dpp(w.x.w, w.y.w, ROR8, 0xF, 0xC, false);
+    r.s4 = __builtin_amdgcn_update_dpp(w.y.x, w.x.x, ROR8, 0xF, 0x3, false);
+    r.s5 = __builtin_amdgcn_update_dpp(w.y.y, w.x.y, ROR8, 0xF, 0x3, false);
+    r.s6 = __builtin_amdgcn_update_dpp(w.y.z, w.x.z, ROR8, 0xF, 0x3, false);
+    r.s7 = __builtin_amdgcn_update_dpp(w.y.w, w.x.w, ROR8, 0xF, 0x3, false);
+    return r;
+}
+
+// The fp8 activation operand matching wl_frag: bytes [32q, 32q + 32) of the
+// k-block (p = row + k-block + 32q).
+__device__ __forceinline__ v8i ld_afrag(const uint8_t* p) {
     const v4i lo = ld16(p);
-    const v4i hi = ld16(p + 64);
+    const v4i hi = ld16(p + 16);
     v8i r;
     r.s0 = lo.x; r.s1 = lo.y; r.s2 = lo.z; r.s3 = lo.w;
     r.s4 = hi.x; r.s5 = hi.y; r.s6 = hi.z; r.s7 = hi.w;

@@ -19,9 +19,10 @@
 // active experts more waves in flight.
 //
 // Operand layout: lane l feeds row (l % 16) of a 16x128 operand with bytes
-// [16g, 16g+16) and [64+16g, 64+16g+16) of the 128-byte k-block, g = l / 16.
-// A and B use the same mapping, so the k pairing inside the MFMA is exact
-// whatever order the instruction assigns to the 32 bytes of a lane.
+// [32g, 32g+32) of the 128-byte k-block, g = l / 16. The weights arrive as
+// whole 128-byte lines (two non-temporal loads per k-block, exchanged within
+// 16-lane rows by wl_frag where they are consumed); the activation row is
+// read at the same k offsets (ld_afrag).
 //
 // With FRONT_SORT (T <= 64, MT = 1) the kernel also stands in for the sort
 // launch: each wave derives its row tile and its rows' tokens from the top-k
@@ -37,7 +38,7 @@
 
 namespace mimoe {
 
-template <int MT, int D, int NW, int KS = 1, int FRONT = FRONT_NONE>
+template <int MT, int D, int NW, int KS = 1, int FRONT = FRONT_NONE, bool NT = true>
 __global__ __launch_bounds__(64 * NW * KS)
 __attribute__((amdgpu_waves_per_eu(FRONT != FRONT_NONE && KS == 4 ? 5 : 1)))
 void gemm1_stream_kernel(Plan p, const uint8_t* __restrict__ hs, const float* __restrict__ hs_scale,
@@ -105,16 +106,20 @@ void gemm1_stream_kernel(Plan p, const uint8_t* __restrict__ hs, const float* __
     const int wc = wave % NW;         // column group
     const int ks = wave / NW;         // k split: k-blocks [ks*KB, ks*KB + KB)
     const int j0 = blockIdx.x * (16 * NW) + wc * 16;
-    const uint8_t* bg_ptr = w1 + ((size_t)e * N1 + j0 + r) * H + (size_t)ks * KB * BLK + g * 16;
-    const uint8_t* bu_ptr = w1 + ((size_t)e * N1 + I + j0 + r) * H + (size_t)ks * KB * BLK + g * 16;
+    // weights of expert e through a buffer resource: gate rows, then up rows I further
+    e = __builtin_amdgcn_readfirstlane(e);
+    const __amdgpu_buffer_rsrc_t wr = wrsrc(w1 + (size_t)e * N1 * H, (uint32_t)((size_t)N1 * H));
+    const uint32_t bg_off = (uint32_t)((size_t)j0 * H + (size_t)ks * KB * BLK + wl_off(lane, H));
+    const uint32_t bu_off = bg_off + (uint32_t)((size_t)I * H);
     const uint8_t* a_ptr[MT];
 #pragma unroll
-    for (int i = 0; i < MT; ++i) a_ptr[i] = hs + (size_t)tok[i] * H + ks * KB * BLK + g * 16;
+    for (int i = 0; i < MT; ++i) a_ptr[i] = hs + (size_t)tok[i] * H + ks * KB * BLK + g * 32;
     const float* sbg_ptr = w1s + ((size_t)e * N1B + j0 / BLK) * HB + ks * KB;
     const float* sbu_ptr = w1s + ((size_t)e * N1B + (I + j0) / BLK) * HB + ks * KB;
     const float (*sa_k)[BM] = sa_lds + ks * KB;  // this wave's k-blocks
 
-    v8i bg[D], bu[D], a[D][MT];
+    WRaw bg[D], bu[D];
+    v8i a[D][MT];
     v4f accg[MT], accu[MT];
     const v4f zero = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
@@ -125,10 +130,12 @@ void gemm1_stream_kernel(Plan p, const uint8_t* __restrict__ hs, const float* __
     auto compute = [&](int d, int kb) __attribute__((always_inline)) {
         const float sg = sbg_ptr[kb];
         const float su = sbu_ptr[kb];
+        const v8i fg = wl_frag(bg[d]);
+        const v8i fu = wl_frag(bu[d]);
 #pragma unroll
         for (int i = 0; i < MT; ++i) {
-            const v4f pg = mfma_f8_16x16x128(a[d][i], bg[d], zero);
-            const v4f pu = mfma_f8_16x16x128(a[d][i], bu[d], zero);
+            const v4f pg = mfma_f8_16x16x128(a[d][i], fg, zero);
+            const v4f pu = mfma_f8_16x16x128(a[d][i], fu, zero);
             const float4 sa4 = *reinterpret_cast<const float4*>(&sa_k[kb][i * 16 + g * 4]);
             accg[i][0] += pg[0] * (sa4.x * sg);
             accg[i][1] += pg[1] * (sa4.y * sg);
@@ -142,10 +149,10 @@ void gemm1_stream_kernel(Plan p, const uint8_t* __restrict__ hs, const float* __
     };
     auto load = [&](int d, int kb) __attribute__((always_inline)) {
         const int nk = kb * BLK;
-        bg[d] = ld_frag(bg_ptr + nk);
-        bu[d] = ld_frag(bu_ptr + nk);
+        bg[d] = ld_wraw<NT>(wr, bg_off + nk, 8 * H);
+        bu[d] = ld_wraw<NT>(wr, bu_off + nk, 8 * H);
 #pragma unroll
-        for (int i = 0; i < MT; ++i) a[d][i] = ld_frag(a_ptr[i] + nk);
+        for (int i = 0; i < MT; ++i) a[d][i] = ld_afrag(a_ptr[i] + nk);
     };
 
     // Start streaming weights first; the activation scales of the tile go to
@@ -235,8 +242,12 @@ static void launch_stream1(const Plan& p, const uint8_t* hs, const float* hs_sca
                            const uint8_t* w1, const float* w1s, hipStream_t s,
                            const FrontArgs& fa = FrontArgs{}) {
     dim3 grid(I / (16 * NW), max_mtiles(p.T, 16 * MT));
-    hipLaunchKernelGGL((gemm1_stream_kernel<MT, D, NW, KS, FRONT>), grid, dim3(64 * NW * KS), 0, s,
-                       p, hs, hs_scale, w1, w1s, fa);
+    if (wt_nt(p.T, 16 * MT))
+        hipLaunchKernelGGL((gemm1_stream_kernel<MT, D, NW, KS, FRONT, true>), grid, dim3(64 * NW * KS), 0,
+                           s, p, hs, hs_scale, w1, w1s, fa);
+    else
+        hipLaunchKernelGGL((gemm1_stream_kernel<MT, D, NW, KS, FRONT, false>), grid, dim3(64 * NW * KS),
+                           0, s, p, hs, hs_scale, w1, w1s, fa);
 }
 
 bool gemm1_routes_supported(int T, int variant) {

@@ -27,9 +27,9 @@
 // the sort's tables for GEMM2 and the combine.
 //
 // Operand layout as in the stream kernel: lane l feeds row (l % 16) of a
-// 16x128 operand with bytes [16g, 16g+16) and [64+16g, 64+16g+16) of the
-// k-block, g = l / 16. LDS rows are 128 bytes with chunk c of row r at
-// position c ^ swz8(r).
+// 16x128 operand with bytes [32g, 32g+32) of the k-block, g = l / 16 (whole-
+// line weight loads, wl_frag). LDS rows are 128 bytes with chunk c of row r
+// at position c ^ swz8(r); a lane reads chunks 2g and 2g + 1.
 #include "sort_impl.hpp"
 #include "tile_common.hpp"
 
@@ -42,7 +42,7 @@ constexpr int WIDE_NW = 4;                  // waves per workgroup
 constexpr int WIDE_G = 16 * WIDE_NW;        // gate columns per workgroup
 constexpr int WIDE_BM = 64;                 // rows per workgroup (see the launcher)
 
-template <int MTW, int D, int DA, bool SORT = false>
+template <int MTW, int D, int DA, bool SORT, bool NT>
 __global__ __launch_bounds__(64 * WIDE_NW) void gemm1_wide_kernel(Plan p, const uint8_t* __restrict__ hs,
                                                                   const float* __restrict__ hs_scale,
                                                                   const uint8_t* __restrict__ w1,
@@ -168,8 +168,11 @@ __global__ __launch_bounds__(64 * WIDE_NW) void gemm1_wide_kernel(Plan p, const 
     const int r = lane & 15, g = lane >> 4;
 
     // weight fragments of this wave (gate and up rows of W1[e])
-    const uint8_t* bg_ptr = w1 + ((size_t)e * N1 + j0 + r) * H + g * 16;
-    const uint8_t* bu_ptr = w1 + ((size_t)e * N1 + I + j0 + r) * H + g * 16;
+    // weights of expert e through a buffer resource: gate rows, then up rows I further
+    e = __builtin_amdgcn_readfirstlane(e);
+    const __amdgpu_buffer_rsrc_t wr = wrsrc(w1 + (size_t)e * N1 * H, (uint32_t)((size_t)N1 * H));
+    const uint32_t bg_off = (uint32_t)((size_t)j0 * H + wl_off(lane, H));
+    const uint32_t bu_off = bg_off + (uint32_t)((size_t)I * H);
     // 64 gate columns lie inside one 128-column scale block, as do the up ones
     const float* sbg_ptr = w1s + ((size_t)e * N1B + jb / BLK) * HB;
     const float* sbu_ptr = w1s + ((size_t)e * N1B + (I + jb) / BLK) * HB;
@@ -185,7 +188,7 @@ __global__ __launch_bounds__(64 * WIDE_NW) void gemm1_wide_kernel(Plan p, const 
         a_dst[i] = row * BLK + ((ac ^ swz8(row)) << 4);
     }
 
-    v8i bg[D], bu[D];
+    WRaw bg[D], bu[D];
     v4i ast[DA][A_LD];
     float sgs[DA], sus[DA];  // weight scales of the staged k-blocks (uniform)
     v4f accg[MTW], accu[MTW];
@@ -194,8 +197,8 @@ __global__ __launch_bounds__(64 * WIDE_NW) void gemm1_wide_kernel(Plan p, const 
     for (int m = 0; m < MTW; ++m) { accg[m] = zero; accu[m] = zero; }
 
     auto load_w = [&](int d, int kb) __attribute__((always_inline)) {
-        bg[d] = ld_frag(bg_ptr + kb * BLK);
-        bu[d] = ld_frag(bu_ptr + kb * BLK);
+        bg[d] = ld_wraw<NT>(wr, bg_off + kb * BLK, 8 * H);
+        bu[d] = ld_wraw<NT>(wr, bu_off + kb * BLK, 8 * H);
     };
     auto load_a = [&](int s, int kb) __attribute__((always_inline)) {
 #pragma unroll
@@ -215,16 +218,18 @@ __global__ __launch_bounds__(64 * WIDE_NW) void gemm1_wide_kernel(Plan p, const 
     };
     auto compute = [&](int d, int buf) __attribute__((always_inline)) {
         const uint8_t* sA = a_lds[buf];
+        const v8i fg = wl_frag(bg[d]);
+        const v8i fu = wl_frag(bu[d]);
 #pragma unroll
         for (int m = 0; m < MTW; ++m) {
             const int row = m * 16 + r;
             const uint8_t* base = sA + row * BLK;
             const int sw = swz8(row);
-            const v4i lo = lds16(base + ((g ^ sw) << 4));
-            const v4i hi = lds16(base + (((g + 4) ^ sw) << 4));
+            const v4i lo = lds16(base + (((2 * g) ^ sw) << 4));
+            const v4i hi = lds16(base + (((2 * g + 1) ^ sw) << 4));
             const v8i a = (v8i){lo.x, lo.y, lo.z, lo.w, hi.x, hi.y, hi.z, hi.w};
-            const v4f pg = mfma_f8_16x16x128(a, bg[d], zero);
-            const v4f pu = mfma_f8_16x16x128(a, bu[d], zero);
+            const v4f pg = mfma_f8_16x16x128(a, fg, zero);
+            const v4f pu = mfma_f8_16x16x128(a, fu, zero);
             const float4 sg = *reinterpret_cast<const float4*>(&cs_lds[buf][0][m * 16 + g * 4]);
             const float4 su = *reinterpret_cast<const float4*>(&cs_lds[buf][1][m * 16 + g * 4]);
             accg[m][0] += pg[0] * sg.x; accg[m][1] += pg[1] * sg.y;
@@ -310,8 +315,12 @@ hipError_t launch_gemm1_wide(const Plan& p, const uint8_t* hs, const float* hs_s
     // three waves per SIMD. Measured against 32-, 96- and 128-row tiles and
     // 4- to 8-deep rings, more resident waves beat deeper rings here.
     dim3 grid(I / WIDE_G, max_mtiles(p.T, WIDE_BM));
-    hipLaunchKernelGGL((gemm1_wide_kernel<WIDE_BM / 16, 2, 1>), grid, dim3(64 * WIDE_NW), 0, s,
-                       p, hs, hs_scale, w1, w1s, 0);
+    if (wt_nt(p.T, WIDE_BM))
+        hipLaunchKernelGGL((gemm1_wide_kernel<WIDE_BM / 16, 2, 1, false, true>), grid, dim3(64 * WIDE_NW),
+                           0, s, p, hs, hs_scale, w1, w1s, 0);
+    else
+        hipLaunchKernelGGL((gemm1_wide_kernel<WIDE_BM / 16, 2, 1, false, false>), grid,
+                           dim3(64 * WIDE_NW), 0, s, p, hs, hs_scale, w1, w1s, 0);
     return hipGetLastError();
 }
 
@@ -325,8 +334,12 @@ hipError_t launch_gemm1_wide_sorting(const Plan& p, const uint8_t* hs, const flo
     if (p.T <= 0) return hipSuccess;
     if (p.T > WIDE_SORT_MAX_T) return hipErrorInvalidValue;
     dim3 grid(I / WIDE_G, max_mtiles(p.T, WIDE_BM));
-    hipLaunchKernelGGL((gemm1_wide_kernel<WIDE_BM / 16, 2, 1, true>), grid, dim3(64 * WIDE_NW), 0,
-                       s, p, hs, hs_scale, w1, w1s, bm2);
+    if (wt_nt(p.T, WIDE_BM))
+        hipLaunchKernelGGL((gemm1_wide_kernel<WIDE_BM / 16, 2, 1, true, true>), grid, dim3(64 * WIDE_NW),
+                           0, s, p, hs, hs_scale, w1, w1s, bm2);
+    else
+        hipLaunchKernelGGL((gemm1_wide_kernel<WIDE_BM / 16, 2, 1, true, false>), grid,
+                           dim3(64 * WIDE_NW), 0, s, p, hs, hs_scale, w1, w1s, bm2);
     return hipGetLastError();
 }
 

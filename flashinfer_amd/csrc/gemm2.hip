@@ -24,11 +24,12 @@
 // rows go to part (bf16) or part_f32, and with G2_SPLIT the activation is
 // act + act_lo (two bf16 MFMAs per k step against the same bf16 weights).
 //
-// Operand layout: lane l (row l % 16, g = l / 16) loads bytes [16g, 16g+16)
-// and [64+16g, 64+16g+16) of the 128-wide k-block of its weight row; MFMA h
+// Operand layout: lane l (row l % 16, g = l / 16) holds bytes [32g, 32g+32)
+// of the 128-wide k-block of its weight row (whole-line non-temporal loads,
+// exchanged within 16-lane rows by wl_frag where they are consumed); MFMA h
 // (h = 0..3) consumes bytes [8h, 8h+8) of those 32, i.e. k-block offsets
-// 16g + 8h (h < 2) and 64 + 16g + 8(h-2) (h >= 2). The activation operand is
-// loaded with the same k offsets, so A and B always pair the same k.
+// 32g + 8h. The activation operand is loaded with the same k offsets, so A
+// and B always pair the same k.
 #include "common.hpp"
 
 namespace mimoe {
@@ -38,13 +39,12 @@ struct Frag16 {
 };
 
 __device__ __forceinline__ Frag16 ld_act(const uint16_t* row, int kb, int g) {
-    const uint16_t* p0 = row + kb * BLK + g * 16;
-    const uint16_t* p1 = row + kb * BLK + 64 + g * 16;
+    const uint16_t* p0 = row + kb * BLK + g * 32;
     Frag16 f;
     f.c0 = ld16(p0);
     f.c1 = ld16(p0 + 8);
-    f.c2 = ld16(p1);
-    f.c3 = ld16(p1 + 8);
+    f.c2 = ld16(p0 + 16);
+    f.c3 = ld16(p0 + 24);
     return f;
 }
 
@@ -70,7 +70,7 @@ __device__ __forceinline__ v4f mfma_block(const Frag16& a, const Frag16& al, con
     return acc;
 }
 
-template <int MT, int D, int NW, int NQ, int MODE, int KS>
+template <int MT, int D, int NW, int NQ, int MODE, int KS, bool NT>
 __global__ __launch_bounds__(64 * NW * KS) void gemm2_stream_kernel(
     Plan p, const uint8_t* __restrict__ w2, const float* __restrict__ w2s) {
     constexpr int KB = IB / KS;  // k-blocks per wave
@@ -93,9 +93,12 @@ __global__ __launch_bounds__(64 * NW * KS) void gemm2_stream_kernel(
     const int nb = n0 / BLK;  // 128-column scale block of the wave's columns
     const int r = lane & 15, g = lane >> 4;
 
-    const uint8_t* b_ptr[NQ];
+    // weights of expert e through a buffer resource
+    e = __builtin_amdgcn_readfirstlane(e);
+    const __amdgpu_buffer_rsrc_t wr = wrsrc(w2 + (size_t)e * H * I, (uint32_t)((size_t)H * I));
+    uint32_t b_off[NQ];
 #pragma unroll
-    for (int q = 0; q < NQ; ++q) b_ptr[q] = w2 + ((size_t)e * H + n0 + q * 16 + r) * I + g * 16;
+    for (int q = 0; q < NQ; ++q) b_off[q] = (uint32_t)((size_t)(n0 + q * 16) * I + wl_off(lane, I));
     const uint16_t* a_row[MT];
     const uint16_t* al_row[MT];
 #pragma unroll
@@ -106,7 +109,7 @@ __global__ __launch_bounds__(64 * NW * KS) void gemm2_stream_kernel(
     }
     const float* sb_ptr = w2s + ((size_t)e * HB + nb) * IB;
 
-    v8i b[D][NQ];
+    WRaw b[D][NQ];
     Frag16 a[D][MT];
     Frag16 al[D][MT];  // PREC only
     v4f acc[MT][NQ];
@@ -122,7 +125,7 @@ __global__ __launch_bounds__(64 * NW * KS) void gemm2_stream_kernel(
         for (int i = 0; i < MT; ++i) {
 #pragma unroll
             for (int q = 0; q < NQ; ++q) {
-                const v4f pr = mfma_block<PREC>(a[d][i], al[d][i], b[d][q]);
+                const v4f pr = mfma_block<PREC>(a[d][i], al[d][i], wl_frag(b[d][q]));
                 acc[i][q][0] += pr[0] * sb;
                 acc[i][q][1] += pr[1] * sb;
                 acc[i][q][2] += pr[2] * sb;
@@ -132,7 +135,7 @@ __global__ __launch_bounds__(64 * NW * KS) void gemm2_stream_kernel(
     };
     auto load = [&](int d, int kb) __attribute__((always_inline)) {
 #pragma unroll
-        for (int q = 0; q < NQ; ++q) b[d][q] = ld_frag(b_ptr[q] + (kb_first + kb) * BLK);
+        for (int q = 0; q < NQ; ++q) b[d][q] = ld_wraw<NT>(wr, b_off[q] + (kb_first + kb) * BLK, 8 * I);
 #pragma unroll
         for (int i = 0; i < MT; ++i) {
             a[d][i] = ld_act(a_row[i], kb_first + kb, g);
@@ -225,6 +228,17 @@ int gemm2_bm(int variant) {
     }
 }
 
+template <int MT, int D, int NW, int NQ, int MODE, int KS>
+static void launch_stream2_mode(const Plan& p, const uint8_t* w2, const float* w2s, dim3 grid,
+                                dim3 block, hipStream_t s) {
+    if (wt_nt(p.T, 16 * MT))
+        hipLaunchKernelGGL((gemm2_stream_kernel<MT, D, NW, NQ, MODE, KS, true>), grid, block, 0, s, p, w2,
+                           w2s);
+    else
+        hipLaunchKernelGGL((gemm2_stream_kernel<MT, D, NW, NQ, MODE, KS, false>), grid, block, 0, s, p, w2,
+                           w2s);
+}
+
 template <int MT, int D, int NW, int NQ, int KS = 1>
 static void launch_stream2(const Plan& p, const uint8_t* w2, const float* w2s, hipStream_t s) {
     // a ring deeper than the shape's k-blocks allow falls back to 2 deep (or 1)
@@ -233,17 +247,9 @@ static void launch_stream2(const Plan& p, const uint8_t* w2, const float* w2s, h
     dim3 grid(H / (16 * NQ * NW), max_mtiles(p.T, 16 * MT));
     const dim3 block(64 * NW * KS);
     switch (gemm2_mode(p)) {
-        case G2_SPLIT:
-            hipLaunchKernelGGL((gemm2_stream_kernel<MT, DD, NW, NQ, G2_SPLIT, KS>), grid, block, 0, s, p,
-                               w2, w2s);
-            break;
-        case G2_F32:
-            hipLaunchKernelGGL((gemm2_stream_kernel<MT, DD, NW, NQ, G2_F32, KS>), grid, block, 0, s, p,
-                               w2, w2s);
-            break;
-        default:
-            hipLaunchKernelGGL((gemm2_stream_kernel<MT, DD, NW, NQ, G2_BF16, KS>), grid, block, 0, s, p,
-                               w2, w2s);
+        case G2_SPLIT: launch_stream2_mode<MT, DD, NW, NQ, G2_SPLIT, KS>(p, w2, w2s, grid, block, s); break;
+        case G2_F32: launch_stream2_mode<MT, DD, NW, NQ, G2_F32, KS>(p, w2, w2s, grid, block, s); break;
+        default: launch_stream2_mode<MT, DD, NW, NQ, G2_BF16, KS>(p, w2, w2s, grid, block, s);
     }
 }
 

@@ -37,7 +37,7 @@ __device__ __forceinline__ UnitInfo unit_info(const int* meta, int u) {
     return r;
 }
 
-template <int D, int KS, bool PREC>
+template <int D, int KS, bool PREC, bool NT>
 __global__ __launch_bounds__(256) void gemm2_combine_kernel(Plan p, const uint8_t* __restrict__ w2,
                                                             const float* __restrict__ w2s,
                                                             uint16_t* __restrict__ out) {
@@ -68,7 +68,7 @@ __global__ __launch_bounds__(256) void gemm2_combine_kernel(Plan p, const uint8_
     float* my_acc = acc_lds + wave * T * 16;
 
     if (nsteps > 0) {
-        v8i b[D];
+        WRaw b[D];
         v4i a[D][4];
         v4i al[D][4];  // PREC only
         // Per-tile data, fetched when the load side enters a tile (D steps
@@ -100,20 +100,21 @@ __global__ __launch_bounds__(256) void gemm2_combine_kernel(Plan p, const uint8_
             // step s: k-block kb of the wave's (s / KBW)-th tile
             const int kb = kb0 + s % KBW;
             if (s % KBW == 0 && s > 0) fetch_unit(u0 + ustep * (s / KBW));
-            const uint8_t* bp = w2 + ((size_t)lu.e * H + n0 + r) * I + g * 16 + kb * BLK;
-            b[d] = ld_frag(bp);
-            const size_t ao = (size_t)(lu.row0 + min(r, lu.nrows - 1)) * I + kb * BLK + g * 16;
+            // whole-line weight loads (wl_frag), activation at the same k offsets
+            const __amdgpu_buffer_rsrc_t wr = wrsrc(w2 + (size_t)lu.e * H * I, (uint32_t)((size_t)H * I));
+            b[d] = ld_wraw<NT>(wr, (uint32_t)((size_t)n0 * I + wl_off(lane, I) + kb * BLK), 8 * I);
+            const size_t ao = (size_t)(lu.row0 + min(r, lu.nrows - 1)) * I + kb * BLK + g * 32;
             const uint16_t* ap = p.act + ao;
             a[d][0] = ld16(ap);
             a[d][1] = ld16(ap + 8);
-            a[d][2] = ld16(ap + 64);
-            a[d][3] = ld16(ap + 72);
+            a[d][2] = ld16(ap + 16);
+            a[d][3] = ld16(ap + 24);
             if constexpr (PREC) {
                 const uint16_t* lp = p.act_lo + ao;
                 al[d][0] = ld16(lp);
                 al[d][1] = ld16(lp + 8);
-                al[d][2] = ld16(lp + 64);
-                al[d][3] = ld16(lp + 72);
+                al[d][2] = ld16(lp + 16);
+                al[d][3] = ld16(lp + 24);
             }
         };
         auto compute = [&](int d, int s) __attribute__((always_inline)) {
@@ -128,10 +129,11 @@ __global__ __launch_bounds__(256) void gemm2_combine_kernel(Plan p, const uint8_
             const float sb = __builtin_bit_cast(
                 float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, cu_sb), kb));
             v4f pr = {0.f, 0.f, 0.f, 0.f};
-            const v4i b0 = fp8x8_to_bf16x8((uint32_t)b[d].s0, (uint32_t)b[d].s1);
-            const v4i b1 = fp8x8_to_bf16x8((uint32_t)b[d].s2, (uint32_t)b[d].s3);
-            const v4i b2 = fp8x8_to_bf16x8((uint32_t)b[d].s4, (uint32_t)b[d].s5);
-            const v4i b3 = fp8x8_to_bf16x8((uint32_t)b[d].s6, (uint32_t)b[d].s7);
+            const v8i bf = wl_frag(b[d]);
+            const v4i b0 = fp8x8_to_bf16x8((uint32_t)bf.s0, (uint32_t)bf.s1);
+            const v4i b1 = fp8x8_to_bf16x8((uint32_t)bf.s2, (uint32_t)bf.s3);
+            const v4i b2 = fp8x8_to_bf16x8((uint32_t)bf.s4, (uint32_t)bf.s5);
+            const v4i b3 = fp8x8_to_bf16x8((uint32_t)bf.s6, (uint32_t)bf.s7);
             v4f pl = pr;  // PREC: the act_lo products, a chain of their own
             if constexpr (PREC) {
                 pl = mfma_bf16_16x16x32(__builtin_bit_cast(v8bf, al[d][0]), __builtin_bit_cast(v8bf, b0), pl);
@@ -185,32 +187,41 @@ constexpr int FUSED_MAX_T = 256;
 
 bool gemm2_combine_supported(int T) { return T > 0 && T <= FUSED_MAX_T; }
 
+// One launch of the kernel for the call's activation form and weight load
+// policy (non-temporal while no expert can hold a second 16-row tile).
+template <int D, int KS>
+static void launch_combine(const Plan& p, const uint8_t* w2, const float* w2s, uint16_t* out,
+                           hipStream_t s) {
+    const size_t lds = (size_t)4 * p.T * 16 * sizeof(float);
+    const bool nt = p.T <= 16;
+    if (p.act_lo && nt)
+        hipLaunchKernelGGL((gemm2_combine_kernel<D, KS, true, true>), dim3(H / 16), dim3(256), lds, s, p,
+                           w2, w2s, out);
+    else if (p.act_lo)
+        hipLaunchKernelGGL((gemm2_combine_kernel<D, KS, true, false>), dim3(H / 16), dim3(256), lds, s, p,
+                           w2, w2s, out);
+    else if (nt)
+        hipLaunchKernelGGL((gemm2_combine_kernel<D, KS, false, true>), dim3(H / 16), dim3(256), lds, s, p,
+                           w2, w2s, out);
+    else
+        hipLaunchKernelGGL((gemm2_combine_kernel<D, KS, false, false>), dim3(H / 16), dim3(256), lds, s,
+                           p, w2, w2s, out);
+}
+
 hipError_t launch_gemm2_combine(const Plan& p, const uint8_t* w2, const float* w2s, uint16_t* out,
                                 hipStream_t s) {
     if (p.T <= 0) return hipSuccess;
-    const size_t lds = (size_t)4 * p.T * 16 * sizeof(float);
     constexpr int D = IB % 4 == 0 ? 4 : 2;  // ring depth must divide the shape's k-blocks
-    if (p.act_lo)
-        hipLaunchKernelGGL((gemm2_combine_kernel<D, 1, true>), dim3(H / 16), dim3(256), lds, s, p, w2,
-                           w2s, out);
-    else
-        hipLaunchKernelGGL((gemm2_combine_kernel<D, 1, false>), dim3(H / 16), dim3(256), lds, s, p,
-                           w2, w2s, out);
+    launch_combine<D, 1>(p, w2, w2s, out, s);
     return hipGetLastError();
 }
 
 hipError_t launch_gemm2_combine_ks(const Plan& p, const uint8_t* w2, const float* w2s,
                                    uint16_t* out, hipStream_t s) {
     if (p.T <= 0) return hipSuccess;
-    const size_t lds = (size_t)4 * p.T * 16 * sizeof(float);
     constexpr int KBW = IB / 4;
     constexpr int D = (KBW % 2 == 0 && KBW > 2) ? 2 : 1;  // divides a wave's k-blocks, below them
-    if (p.act_lo)
-        hipLaunchKernelGGL((gemm2_combine_kernel<D, 4, true>), dim3(H / 16), dim3(256), lds, s, p, w2,
-                           w2s, out);
-    else
-        hipLaunchKernelGGL((gemm2_combine_kernel<D, 4, false>), dim3(H / 16), dim3(256), lds, s, p,
-                           w2, w2s, out);
+    launch_combine<D, 4>(p, w2, w2s, out, s);
     return hipGetLastError();
 }
 

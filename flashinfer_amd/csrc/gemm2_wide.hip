@@ -18,9 +18,10 @@
 // the MFMAs of both halves against the same bf16 weights.
 //
 // Operand k order (identical for A and B, so the pairing is exact): lane
-// (r = l%16, g = l/16) holds k-block offsets 16g+[0,16) and 64+16g+[0,16);
-// MFMA h uses offsets 16g+8h (h<2) and 64+16g+8(h-2) (h>=2). LDS activation
-// rows are 256 bytes (16 chunks) with chunk c at position c ^ (row & 15).
+// (r = l%16, g = l/16) holds k-block offsets 32g+[0,32) (whole-line weight
+// loads, wl_frag); MFMA h uses offsets 32g+8h. LDS activation rows are 256
+// bytes (16 chunks of 8 bf16) with chunk c at position c ^ (row & 15); a
+// lane reads chunks 4g..4g+3.
 #include "tile_common.hpp"
 
 namespace mimoe {
@@ -58,7 +59,13 @@ __global__ __launch_bounds__(64 * W2_NW) void gemm2_wide_kernel(Plan p, const ui
     const int n0 = nb0 + wave * 16;      // first output column of this wave
     const int r = lane & 15, g = lane >> 4;
 
-    const uint8_t* b_ptr = w2 + ((size_t)e * H + n0 + r) * I + g * 16;
+    // weights of expert e through a buffer resource, plain loads: the 32-row
+    // tiles run at 177 <= T <= 256, where the non-temporal hint gained nothing
+    // with random routing (76.8 against 76.9 us at T=256) and cost 20 % with
+    // every token on the same 8 experts (8 row tiles each)
+    e = __builtin_amdgcn_readfirstlane(e);
+    const __amdgpu_buffer_rsrc_t wr = wrsrc(w2 + (size_t)e * H * I, (uint32_t)((size_t)H * I));
+    const uint32_t b_off = (uint32_t)((size_t)n0 * I + wl_off(lane, I));
     const float* sb_ptr = w2s + ((size_t)e * HB + nb0 / BLK) * IB;
 
     // activation loader: thread t copies chunk t%16 of rows t/16 + 16i
@@ -77,14 +84,16 @@ __global__ __launch_bounds__(64 * W2_NW) void gemm2_wide_kernel(Plan p, const ui
     // prologue (every thread stores, so the load is not sunk into a branch).
     const float w_row = p.sorted_w[row0 + min(tid, nrows - 1)];
 
-    v8i b[D];
+    WRaw b[D];
     v4i ast[DA][A_LD];
     v4f acc[MTW];
     const v4f zero = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int m = 0; m < MTW; ++m) acc[m] = zero;
 
-    auto load_w = [&](int d, int kb) __attribute__((always_inline)) { b[d] = ld_frag(b_ptr + kb * BLK); };
+    auto load_w = [&](int d, int kb) __attribute__((always_inline)) {
+        b[d] = ld_wraw<false>(wr, b_off + kb * BLK, 8 * I);
+    };
     auto load_a = [&](int s, int kb) __attribute__((always_inline)) {
 #pragma unroll
         for (int i = 0; i < A_LD; ++i) ast[s][i] = ld16(a_src[i] + kb * ROW_BYTES);
@@ -94,7 +103,7 @@ __global__ __launch_bounds__(64 * W2_NW) void gemm2_wide_kernel(Plan p, const ui
         for (int i = 0; i < A_LD; ++i) *reinterpret_cast<v4i*>(&a_lds[buf][a_dst[i]]) = ast[s][i];
     };
     auto compute = [&](int d, int buf, float sb) __attribute__((always_inline)) {
-        const v8i w = b[d];
+        const v8i w = wl_frag(b[d]);
         const v4i b0 = fp8x8_to_bf16x8((uint32_t)w.s0, (uint32_t)w.s1);
         const v4i b1 = fp8x8_to_bf16x8((uint32_t)w.s2, (uint32_t)w.s3);
         const v4i b2 = fp8x8_to_bf16x8((uint32_t)w.s4, (uint32_t)w.s5);
@@ -105,18 +114,18 @@ __global__ __launch_bounds__(64 * W2_NW) void gemm2_wide_kernel(Plan p, const ui
             const int row = m * 16 + r;
             const uint8_t* base = sA + row * ROW_BYTES;
             const int sw = swz16(row);
-            const v4i a0 = lds16(base + (((2 * g) ^ sw) << 4));
-            const v4i a1 = lds16(base + (((2 * g + 1) ^ sw) << 4));
-            const v4i a2 = lds16(base + (((8 + 2 * g) ^ sw) << 4));
-            const v4i a3 = lds16(base + (((9 + 2 * g) ^ sw) << 4));
+            const v4i a0 = lds16(base + (((4 * g) ^ sw) << 4));
+            const v4i a1 = lds16(base + (((4 * g + 1) ^ sw) << 4));
+            const v4i a2 = lds16(base + (((4 * g + 2) ^ sw) << 4));
+            const v4i a3 = lds16(base + (((4 * g + 3) ^ sw) << 4));
             v4f pl = zero;  // act_lo products: a chain of their own
             if constexpr (PREC) {
                 // act_lo row m*16+r sits BM rows further (same swizzle: BM % 16 == 0)
                 const uint8_t* lbase = base + BM * ROW_BYTES;
-                const v4i l0 = lds16(lbase + (((2 * g) ^ sw) << 4));
-                const v4i l1 = lds16(lbase + (((2 * g + 1) ^ sw) << 4));
-                const v4i l2 = lds16(lbase + (((8 + 2 * g) ^ sw) << 4));
-                const v4i l3 = lds16(lbase + (((9 + 2 * g) ^ sw) << 4));
+                const v4i l0 = lds16(lbase + (((4 * g) ^ sw) << 4));
+                const v4i l1 = lds16(lbase + (((4 * g + 1) ^ sw) << 4));
+                const v4i l2 = lds16(lbase + (((4 * g + 2) ^ sw) << 4));
+                const v4i l3 = lds16(lbase + (((4 * g + 3) ^ sw) << 4));
                 pl = mfma_bf16_16x16x32(__builtin_bit_cast(v8bf, l0), __builtin_bit_cast(v8bf, b0), pl);
                 pl = mfma_bf16_16x16x32(__builtin_bit_cast(v8bf, l1), __builtin_bit_cast(v8bf, b1), pl);
                 pl = mfma_bf16_16x16x32(__builtin_bit_cast(v8bf, l2), __builtin_bit_cast(v8bf, b2), pl);

@@ -16,8 +16,11 @@ typedef __bf16 v8bf __attribute__((ext_vector_type(8)));
 constexpr int UNROLL = 8;  // independent 16-byte loads in flight per lane
 
 // Each wave streams its own contiguous span of `per_wave` vectors (a
-// multiple of 64): one load instruction covers 1 KB, UNROLL of them in
-// flight. Contiguous spans per wave beat a grid-wide stride by ~8 %.
+// multiple of 64): one load instruction covers 1 KB (8 whole 128-byte
+// lines), UNROLL of them in flight. Contiguous spans per wave beat a
+// grid-wide stride by ~8 %; non-temporal loads (the streaming hint, as the
+// operator's weight streams use) read ~13 % faster than plain ones here.
+__device__ __forceinline__ v4i ld_nt(const v4i* p) { return __builtin_nontemporal_load(p); }
 __device__ __forceinline__ void wave_span(size_t n, size_t per_wave, size_t& i, size_t& end) {
     const size_t wave = (size_t)blockIdx.x * 4 + (threadIdx.x >> 6);
     i = wave * per_wave + (threadIdx.x & 63);
@@ -33,11 +36,11 @@ __global__ __launch_bounds__(256) void read_kernel(const v4i* __restrict__ p, si
     for (; i + (UNROLL - 1) * 64 < end; i += UNROLL * 64) {
         v4i r[UNROLL];
 #pragma unroll
-        for (int u = 0; u < UNROLL; ++u) r[u] = p[i + u * 64];
+        for (int u = 0; u < UNROLL; ++u) r[u] = ld_nt(&p[i + u * 64]);
 #pragma unroll
         for (int u = 0; u < UNROLL; ++u) acc ^= r[u];
     }
-    for (; i < end; i += 64) acc ^= p[i];
+    for (; i < end; i += 64) acc ^= ld_nt(&p[i]);
     if ((acc.x ^ acc.y ^ acc.z ^ acc.w) == 0x5EED1234) sink[0] = 1;
 }
 
@@ -48,11 +51,11 @@ __global__ __launch_bounds__(256) void copy_kernel(v4i* __restrict__ d, const v4
     for (; i + (UNROLL - 1) * 64 < end; i += UNROLL * 64) {
         v4i r[UNROLL];
 #pragma unroll
-        for (int u = 0; u < UNROLL; ++u) r[u] = s[i + u * 64];
+        for (int u = 0; u < UNROLL; ++u) r[u] = ld_nt(&s[i + u * 64]);
 #pragma unroll
         for (int u = 0; u < UNROLL; ++u) d[i + u * 64] = r[u];
     }
-    for (; i < end; i += 64) d[i] = s[i];
+    for (; i < end; i += 64) d[i] = ld_nt(&s[i]);
 }
 
 // Vectors per wave so that workgroups x 4 waves cover n, rounded up to 64.

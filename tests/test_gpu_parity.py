@@ -300,11 +300,11 @@ def test_random_workloads(i, T, offset, skew, rsf):
 
 # Both sides of every T at which the default kernels change: fused GEMM2+combine
 # (T <= 4), routing inside GEMM1 (T = 1), sort inside GEMM1 (T <= 64), GEMM2 stream
-# shapes (8 / 9), wide GEMM1 with the sort folded in (65..256), GEMM2 stream shapes
-# (128 / 129), wide GEMM2 (177..256), tiled GEMM2 (> 256), chunked two-kernel sort
-# (> 1024), LDS-tiled GEMM1 (> 1536).
-@pytest.mark.parametrize("T", [1, 2, 4, 5, 8, 9, 32, 33, 64, 65, 128, 129, 176, 177, 192, 193, 256,
-                               257, 1024, 1025, 1536, 1537, 2049])
+# shapes (16 / 17; 8 / 9 in smaller layers), wide GEMM1 with the sort folded in
+# (65..256), GEMM2 stream shapes (128 / 129), wide GEMM2 (177..256), tiled GEMM2
+# (> 256), chunked two-kernel sort (> 1024), LDS-tiled GEMM1 (> 1536).
+@pytest.mark.parametrize("T", [1, 2, 4, 5, 8, 9, 16, 17, 32, 33, 64, 65, 128, 129, 176, 177, 192,
+                               193, 256, 257, 1024, 1025, 1536, 1537, 2049])
 def test_variant_boundaries(T):
     log(f"test_variant_boundaries[T={T}]")
     wl = W.make_workload(f"boundary_t{T}", T=T, seed=1000 + T, local_expert_offset=32 * (T % 8))
@@ -407,22 +407,24 @@ def _sort_tables(T):
             "tok_slot": ws[L.tok_slot:L.tok_slot + T * 32].view(torch.int32).clone()}
 
 
-@pytest.mark.parametrize("T,offset,skew", [(1, 0, False), (3, 32, True), (4, 0, False),
-                                           (9, 0, False), (16, 96, False), (33, 224, False),
-                                           (64, 0, False), (64, 32, True), (48, 256, False),
-                                           (65, 0, False), (100, 32, True), (128, 224, False),
-                                           (129, 0, False), (200, 96, False), (256, 32, True),
-                                           (160, 256, False)])
-def test_sort_in_gemm1_matches_sort_launch(T, offset, skew, monkeypatch):
+@pytest.mark.parametrize("T,offset,skew,variant", [
+    (1, 0, False, ""), (1, 0, False, "5,17"), (3, 32, True, "5,17"), (3, 32, True, ""),
+    (4, 0, False, ""), (9, 0, False, ""), (16, 96, False, ""), (33, 224, False, ""),
+    (64, 0, False, ""), (64, 32, True, ""), (48, 256, False, ""), (65, 0, False, ""),
+    (100, 32, True, ""), (128, 224, False, ""), (129, 0, False, ""), (200, 96, False, ""),
+    (256, 32, True, ""), (160, 256, False, "")])
+def test_sort_in_gemm1_matches_sort_launch(T, offset, skew, variant, monkeypatch):
     """GEMM1 finding its row tiles from the top-k ids (and writing the sort's
     tables itself) gives bit-identical output and tables to the separate sort
-    launch, for every GEMM1 kernel that can do it (single-wave workgroups at
-    T = 1, K split up to 64, the wide 64-row tiles from 65 to 256): ragged T,
+    launch, for every GEMM1 kernel that can do it (K split up to 64, single-
+    wave workgroups when asked for, the wide 64-row tiles from 65 to 256): ragged T,
     other shard offsets, several row tiles per expert (skew) and no local
     token at all (offset 256)."""
     from flashinfer_amd import _lib, kernel
-    log(f"test_sort_in_gemm1_matches_sort_launch[T={T}-off={offset}-skew={skew}]")
+    log(f"test_sort_in_gemm1_matches_sort_launch[T={T}-off={offset}-skew={skew}-v={variant}]")
     wl = W.make_workload("sort_in_gemm1", T, 300 + T, local_expert_offset=offset, skew=skew)
+    if variant:
+        monkeypatch.setenv("MI_MOE_VARIANT", variant)
     monkeypatch.setenv("MI_MOE_FUSE_FRONT", "0")
     monkeypatch.setenv("MI_MOE_ROUTE_IN_GEMM1", "0")
     monkeypatch.setenv("MI_MOE_SORT_IN_GEMM1", "0")
@@ -444,20 +446,22 @@ def test_sort_in_gemm1_matches_sort_launch(T, offset, skew, monkeypatch):
         assert int(want["mtile1"][32]) > int((want["expert_off"][1:] > want["expert_off"][:-1]).sum())
 
 
-@pytest.mark.parametrize("T,offset,skew,force", [(1, 0, False, False), (2, 32, True, False),
-                                                 (4, 96, False, False), (7, 0, False, False),
-                                                 (16, 224, False, False), (16, 32, True, False),
-                                                 (12, 256, False, False), (33, 0, False, True),
-                                                 (64, 32, True, True)])
-def test_route_in_gemm1_matches_separate_launches(T, offset, skew, force, monkeypatch):
+@pytest.mark.parametrize("T,offset,skew,force,variant", [
+    (1, 0, False, False, ""), (1, 0, False, False, "5,17"), (2, 32, True, False, ""),
+    (4, 96, False, False, ""), (7, 0, False, False, ""), (16, 224, False, False, ""),
+    (16, 32, True, False, ""), (12, 256, False, False, ""), (33, 0, False, True, ""),
+    (64, 32, True, True, ""), (3, 32, True, True, "5,17"), (64, 0, False, True, "5,17")])
+def test_route_in_gemm1_matches_separate_launches(T, offset, skew, force, variant, monkeypatch):
     """GEMM1 routing every token itself (each workgroup, into LDS), sorting,
     and writing the top-k and the sort tables gives bit-identical output,
     top-k and tables to the routing and sort kernels: both GEMM1 shapes
-    (single-wave workgroups at T = 1, K split above), T up to 64 when forced
-    on, other shard offsets, skewed routing and no local token."""
+    (K split by default, single-wave workgroups when asked for), T up to 64
+    when forced on, other shard offsets, skewed routing and no local token."""
     from flashinfer_amd import _lib, kernel
-    log(f"test_route_in_gemm1_matches_separate_launches[T={T}-off={offset}-skew={skew}]")
+    log(f"test_route_in_gemm1_matches_separate_launches[T={T}-off={offset}-skew={skew}-v={variant}]")
     wl = W.make_workload("route_in_gemm1", T, 400 + T, local_expert_offset=offset, skew=skew)
+    if variant:
+        monkeypatch.setenv("MI_MOE_VARIANT", variant)
     for k in ("MI_MOE_FUSE_FRONT", "MI_MOE_ROUTE_IN_GEMM1", "MI_MOE_SORT_IN_GEMM1"):
         monkeypatch.setenv(k, "0")
     ref = run_gpu(wl, fill=float("nan")).clone()
