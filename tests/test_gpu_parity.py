@@ -249,6 +249,19 @@ def test_skew_all_rows_on_biased_experts():
     assert torch.equal(eoff, want)
 
 
+@pytest.mark.parametrize("T", [16, 64, 256])
+def test_skewed_decode_parity(T):
+    """Every token on the same 8 local experts at decode sizes: each expert
+    holds T rows, so the stream kernels (T = 16, 64) and the wide ones (256)
+    run several row tiles per expert, re-reading its weights, with the load
+    policy of a random batch of that size. Every token against the oracle."""
+    log(f"test_skewed_decode_parity[T={T}]")
+    wl = W.make_workload(f"skew_decode_t{T}", T, 900 + T, local_expert_offset=0, skew=True)
+    _route_check(wl)
+    out = run_gpu(wl, fill=float("nan"))
+    _check_output(wl, out, torch.arange(T))
+
+
 def test_max_tokens_every_slot_local():
     """The largest accepted batch with every token routed to the same 8 local
     experts: S = 8T = 2^20 slots, so the last slots' gathered-row offsets are
@@ -301,10 +314,11 @@ def test_random_workloads(i, T, offset, skew, rsf):
 # Both sides of every T at which the default kernels change: fused GEMM2+combine
 # (T <= 4), routing inside GEMM1 (T = 1), sort inside GEMM1 (T <= 64), GEMM2 stream
 # shapes (16 / 17; 8 / 9 in smaller layers), wide GEMM1 with the sort folded in
-# (65..256), GEMM2 stream shapes (128 / 129), wide GEMM2 (177..256), tiled GEMM2
-# (> 256), chunked two-kernel sort (> 1024), LDS-tiled GEMM1 (> 1536).
+# (65..256), GEMM2 stream shapes and the stream kernels' weight load policy (128 /
+# 129), wide GEMM2 (177..256), tiled GEMM2 (> 256), the wide GEMM1's load policy
+# (512 / 513), chunked two-kernel sort (> 1024), LDS-tiled GEMM1 (> 1536).
 @pytest.mark.parametrize("T", [1, 2, 4, 5, 8, 9, 16, 17, 32, 33, 64, 65, 128, 129, 176, 177, 192,
-                               193, 256, 257, 1024, 1025, 1536, 1537, 2049])
+                               193, 256, 257, 512, 513, 1024, 1025, 1536, 1537, 2049])
 def test_variant_boundaries(T):
     log(f"test_variant_boundaries[T={T}]")
     wl = W.make_workload(f"boundary_t{T}", T=T, seed=1000 + T, local_expert_offset=32 * (T % 8))
