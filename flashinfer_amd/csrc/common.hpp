@@ -199,9 +199,10 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t wrsrc(const void* base, uint32
 // re-read its weights, plain loads keep them in L2 / MALL for the others
 // (with the hint each tile fetched them from HBM again: T=1024 with up to 8
 // row tiles per expert, GEMM1 564 against 475 us). The policy is a template
-// argument picked per launch from T (wt_nt): chosen per workgroup at run
-// time, the two load forms in one loop cost the stream GEMM1 its registers
-// (spills).
+// argument: per workgroup from its expert's row count in the wide GEMM1 and
+// the stream GEMM2 (two copies of the k loop, BoolC below); per launch from
+// T (wt_nt) in the stream GEMM1, whose two-copy form took 69 -> 96 VGPRs
+// (108 without the sort folded in), and in the GEMM2 + combine kernel.
 struct WRaw {
     v4i x, y;
 };
@@ -223,6 +224,14 @@ __device__ __forceinline__ WRaw ld_wraw(__amdgpu_buffer_rsrc_t r, uint32_t off, 
 // with every token on the same 8 experts (T = 64 / 256: 4 row tiles each)
 // 5-7 % slower, the price of not knowing the counts on the host.
 inline bool wt_nt(int64_t T, int bm) { return T * TOPK <= (int64_t)bm * EG / 4; }
+
+// Compile-time bool for `body(BoolC<NT>{})`: a kernel whose register budget
+// allows it runs one of two copies of its k loop per workgroup, picking the
+// load policy from its expert's row count.
+template <bool B>
+struct BoolC {
+    static constexpr bool value = B;
+};
 
 __device__ __forceinline__ v8i wl_frag(const WRaw& w) {
     constexpr int ROR8 = 0x128;  // DPP row_ror:8

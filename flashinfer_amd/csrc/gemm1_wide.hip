@@ -42,7 +42,7 @@ constexpr int WIDE_NW = 4;                  // waves per workgroup
 constexpr int WIDE_G = 16 * WIDE_NW;        // gate columns per workgroup
 constexpr int WIDE_BM = 64;                 // rows per workgroup (see the launcher)
 
-template <int MTW, int D, int DA, bool SORT, bool NT>
+template <int MTW, int D, int DA, bool SORT>
 __global__ __launch_bounds__(64 * WIDE_NW) void gemm1_wide_kernel(Plan p, const uint8_t* __restrict__ hs,
                                                                   const float* __restrict__ hs_scale,
                                                                   const uint8_t* __restrict__ w1,
@@ -68,7 +68,7 @@ __global__ __launch_bounds__(64 * WIDE_NW) void gemm1_wide_kernel(Plan p, const 
     static_assert(THREADS % BM == 0, "scale loader row");
 
     // Row tile, and the tokens of this thread's loader rows and scale row.
-    int e, row0, nrows;
+    int e, row0, nrows, erows;  // erows: the expert's rows over all its row tiles
     int tok_a[A_LD], tok_s;
     if constexpr (SORT) {
         static_assert(WIDE_NW * 64 >= 256 && BM == 64, "4 chunks of 64 tokens, 64-row tiles");
@@ -131,6 +131,7 @@ __global__ __launch_bounds__(64 * WIDE_NW) void gemm1_wide_kernel(Plan p, const 
         const int sfirst = __builtin_amdgcn_readlane(v0 - cnt, ee);
         const int ce = __builtin_amdgcn_readlane(cnt, ee);
         e = ee;
+        erows = ce;
         const int rank0 = (mt - tfirst) * BM;
         row0 = sfirst + rank0;
         nrows = min(BM, ce - rank0);
@@ -158,6 +159,7 @@ __global__ __launch_bounds__(64 * WIDE_NW) void gemm1_wide_kernel(Plan p, const 
         tok_s = row_token(tid % BM);
     } else {
         if (!find_tile(p.meta, META_MTILE1, blockIdx.y, BM, e, row0, nrows)) return;
+        erows = p.meta[META_EXPERT_OFF + e + 1] - p.meta[META_EXPERT_OFF + e];
 #pragma unroll
         for (int i = 0; i < A_LD; ++i)
             tok_a[i] = p.sorted_tok[row0 + min((tid >> 3) + ROWS_PER_PASS * i, nrows - 1)];
@@ -188,113 +190,125 @@ __global__ __launch_bounds__(64 * WIDE_NW) void gemm1_wide_kernel(Plan p, const 
         a_dst[i] = row * BLK + ((ac ^ swz8(row)) << 4);
     }
 
-    WRaw bg[D], bu[D];
-    v4i ast[DA][A_LD];
-    float sgs[DA], sus[DA];  // weight scales of the staged k-blocks (uniform)
     v4f accg[MTW], accu[MTW];
     const v4f zero = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int m = 0; m < MTW; ++m) { accg[m] = zero; accu[m] = zero; }
 
-    auto load_w = [&](int d, int kb) __attribute__((always_inline)) {
-        bg[d] = ld_wraw<NT>(wr, bg_off + kb * BLK, 8 * H);
-        bu[d] = ld_wraw<NT>(wr, bu_off + kb * BLK, 8 * H);
-    };
-    auto load_a = [&](int s, int kb) __attribute__((always_inline)) {
-#pragma unroll
-        for (int i = 0; i < A_LD; ++i) ast[s][i] = ld16(a_src[i] + kb * BLK);
-        sgs[s] = sbg_ptr[kb];
-        sus[s] = sbu_ptr[kb];
-    };
-    auto store_a = [&](int s, int buf, int kb) __attribute__((always_inline)) {
-#pragma unroll
-        for (int i = 0; i < A_LD; ++i)
-            *reinterpret_cast<v4i*>(&a_lds[buf][a_dst[i]]) = ast[s][i];
-        if (tid < BM) {
-            const float sa = sa_lds[kb][tid];
-            cs_lds[buf][0][tid] = sa * sgs[s];
-            cs_lds[buf][1][tid] = sa * sus[s];
-        }
-    };
-    auto compute = [&](int d, int buf) __attribute__((always_inline)) {
-        const uint8_t* sA = a_lds[buf];
-        const v8i fg = wl_frag(bg[d]);
-        const v8i fu = wl_frag(bu[d]);
-#pragma unroll
-        for (int m = 0; m < MTW; ++m) {
-            const int row = m * 16 + r;
-            const uint8_t* base = sA + row * BLK;
-            const int sw = swz8(row);
-            const v4i lo = lds16(base + (((2 * g) ^ sw) << 4));
-            const v4i hi = lds16(base + (((2 * g + 1) ^ sw) << 4));
-            const v8i a = (v8i){lo.x, lo.y, lo.z, lo.w, hi.x, hi.y, hi.z, hi.w};
-            const v4f pg = mfma_f8_16x16x128(a, fg, zero);
-            const v4f pu = mfma_f8_16x16x128(a, fu, zero);
-            const float4 sg = *reinterpret_cast<const float4*>(&cs_lds[buf][0][m * 16 + g * 4]);
-            const float4 su = *reinterpret_cast<const float4*>(&cs_lds[buf][1][m * 16 + g * 4]);
-            accg[m][0] += pg[0] * sg.x; accg[m][1] += pg[1] * sg.y;
-            accg[m][2] += pg[2] * sg.z; accg[m][3] += pg[3] * sg.w;
-            accu[m][0] += pu[0] * su.x; accu[m][1] += pu[1] * su.y;
-            accu[m][2] += pu[2] * su.z; accu[m][3] += pu[3] * su.w;
-        }
-        // The products are pure arithmetic, which the compiler would
-        // otherwise sink below the following barriers into the last unrolled
-        // k-block, keeping every LDS fragment of the unrolled body live.
-        // Naming the accumulators here pins each k-block's work before its
-        // barrier.
-#pragma unroll
-        for (int m = 0; m < MTW; ++m) asm volatile("" : "+v"(accg[m]), "+v"(accu[m]));
-    };
+    // The k loop, with the weight load policy of the tile's expert (NT: non-
+    // temporal, when this is its only row tile). Measured against a policy
+    // per launch from T: level at T = 100 / 256 / 512 with random routing,
+    // 13 % faster at T=1024 offset 64 (399 slots, one tile per expert), 5 %
+    // with every token on the same 8 experts at T=256; the two copies of the
+    // loop leave the kernel at 136 VGPRs, no spills.
+    auto body = [&](auto nt) __attribute__((always_inline)) {
+        constexpr bool NT = decltype(nt)::value;
+        WRaw bg[D], bu[D];
+        v4i ast[DA][A_LD];
+        float sgs[DA], sus[DA];  // weight scales of the staged k-blocks (uniform)
 
-    // Activation scales of every k-block into LDS once: in the loop they come
-    // from LDS, so no vector load there waits on anything but its own data.
-    for (int i = tid; i < HB * BM; i += THREADS) {
-        const int kb = i / BM, m = i % BM;  // m == tid % BM: the row of tok_s
-        sa_lds[kb][m] = hs_scale[(size_t)kb * p.T + tok_s];
-    }
-    __syncthreads();
-
-    // Prologue: the loads that iterations -D..-1 of the loop would have
-    // issued, in their order (iteration j loads A(j+1+DA), then W(j+D); the
-    // store of A(0) to LDS buffer 0 belongs to iteration -1), so every wait in
-    // the loop sees as many younger loads on the first trip as on later ones.
-    static_assert(D > DA, "prologue order");
-    // (sched_barrier keeps the scheduler from reordering the groups.)
+        auto load_w = [&](int d, int kb) __attribute__((always_inline)) {
+            bg[d] = ld_wraw<NT>(wr, bg_off + kb * BLK, 8 * H);
+            bu[d] = ld_wraw<NT>(wr, bu_off + kb * BLK, 8 * H);
+        };
+        auto load_a = [&](int s, int kb) __attribute__((always_inline)) {
 #pragma unroll
-    for (int d = 0; d < D; ++d) {
-        const int a = d - (D - DA - 1);
-        if (a >= 0) {
-            if (a == DA) store_a(0, 0, 0);  // frees staging slot 0 for A(DA)
-            load_a(a % DA, a);
+            for (int i = 0; i < A_LD; ++i) ast[s][i] = ld16(a_src[i] + kb * BLK);
+            sgs[s] = sbg_ptr[kb];
+            sus[s] = sbu_ptr[kb];
+        };
+        auto store_a = [&](int s, int buf, int kb) __attribute__((always_inline)) {
+#pragma unroll
+            for (int i = 0; i < A_LD; ++i)
+                *reinterpret_cast<v4i*>(&a_lds[buf][a_dst[i]]) = ast[s][i];
+            if (tid < BM) {
+                const float sa = sa_lds[kb][tid];
+                cs_lds[buf][0][tid] = sa * sgs[s];
+                cs_lds[buf][1][tid] = sa * sus[s];
+            }
+        };
+        auto compute = [&](int d, int buf) __attribute__((always_inline)) {
+            const uint8_t* sA = a_lds[buf];
+            const v8i fg = wl_frag(bg[d]);
+            const v8i fu = wl_frag(bu[d]);
+#pragma unroll
+            for (int m = 0; m < MTW; ++m) {
+                const int row = m * 16 + r;
+                const uint8_t* base = sA + row * BLK;
+                const int sw = swz8(row);
+                const v4i lo = lds16(base + (((2 * g) ^ sw) << 4));
+                const v4i hi = lds16(base + (((2 * g + 1) ^ sw) << 4));
+                const v8i a = (v8i){lo.x, lo.y, lo.z, lo.w, hi.x, hi.y, hi.z, hi.w};
+                const v4f pg = mfma_f8_16x16x128(a, fg, zero);
+                const v4f pu = mfma_f8_16x16x128(a, fu, zero);
+                const float4 sg = *reinterpret_cast<const float4*>(&cs_lds[buf][0][m * 16 + g * 4]);
+                const float4 su = *reinterpret_cast<const float4*>(&cs_lds[buf][1][m * 16 + g * 4]);
+                accg[m][0] += pg[0] * sg.x; accg[m][1] += pg[1] * sg.y;
+                accg[m][2] += pg[2] * sg.z; accg[m][3] += pg[3] * sg.w;
+                accu[m][0] += pu[0] * su.x; accu[m][1] += pu[1] * su.y;
+                accu[m][2] += pu[2] * su.z; accu[m][3] += pu[3] * su.w;
+            }
+            // The products are pure arithmetic, which the compiler would
+            // otherwise sink below the following barriers into the last unrolled
+            // k-block, keeping every LDS fragment of the unrolled body live.
+            // Naming the accumulators here pins each k-block's work before its
+            // barrier.
+#pragma unroll
+            for (int m = 0; m < MTW; ++m) asm volatile("" : "+v"(accg[m]), "+v"(accu[m]));
+        };
+
+        // Activation scales of every k-block into LDS once: in the loop they come
+        // from LDS, so no vector load there waits on anything but its own data.
+        for (int i = tid; i < HB * BM; i += THREADS) {
+            const int kb = i / BM, m = i % BM;  // m == tid % BM: the row of tok_s
+            sa_lds[kb][m] = hs_scale[(size_t)kb * p.T + tok_s];
+        }
+        __syncthreads();
+
+        // Prologue: the loads that iterations -D..-1 of the loop would have
+        // issued, in their order (iteration j loads A(j+1+DA), then W(j+D); the
+        // store of A(0) to LDS buffer 0 belongs to iteration -1), so every wait in
+        // the loop sees as many younger loads on the first trip as on later ones.
+        static_assert(D > DA, "prologue order");
+        // (sched_barrier keeps the scheduler from reordering the groups.)
+#pragma unroll
+        for (int d = 0; d < D; ++d) {
+            const int a = d - (D - DA - 1);
+            if (a >= 0) {
+                if (a == DA) store_a(0, 0, 0);  // frees staging slot 0 for A(DA)
+                load_a(a % DA, a);
+                __builtin_amdgcn_sched_barrier(0);
+            }
+            load_w(d, d);
             __builtin_amdgcn_sched_barrier(0);
         }
-        load_w(d, d);
-        __builtin_amdgcn_sched_barrier(0);
-    }
-    __syncthreads();
+        __syncthreads();
 
-    // k-block kb: stage kb+1 into the other LDS buffer (its staging slot is
-    // refilled with kb+1+DA), consume kb, refill the weight ring with kb+D.
-    // Loads past the last k-block re-read the last one; their values are
-    // never consumed.
-    constexpr int U = lcm_c(lcm_c(D, DA), 2);  // ring slots and LDS buffer repeat every U
-    static_assert(HB % U == 0, "unroll");
+        // k-block kb: stage kb+1 into the other LDS buffer (its staging slot is
+        // refilled with kb+1+DA), consume kb, refill the weight ring with kb+D.
+        // Loads past the last k-block re-read the last one; their values are
+        // never consumed.
+        constexpr int U = lcm_c(lcm_c(D, DA), 2);  // ring slots and LDS buffer repeat every U
+        static_assert(HB % U == 0, "unroll");
 #pragma unroll 1
-    for (int kb0 = 0; kb0 < HB; kb0 += U) {
+        for (int kb0 = 0; kb0 < HB; kb0 += U) {
 #pragma unroll
-        for (int u = 0; u < U; ++u) {
-            const int kb = kb0 + u;
-            const int buf = u & 1;
-            const int s = (u + 1) % DA;  // staging slot holding k-block kb+1
-            if (kb + 1 < HB) {
-                store_a(s, buf ^ 1, kb + 1);
-                load_a(s, min(kb + 1 + DA, HB - 1));
+            for (int u = 0; u < U; ++u) {
+                const int kb = kb0 + u;
+                const int buf = u & 1;
+                const int s = (u + 1) % DA;  // staging slot holding k-block kb+1
+                if (kb + 1 < HB) {
+                    store_a(s, buf ^ 1, kb + 1);
+                    load_a(s, min(kb + 1 + DA, HB - 1));
+                }
+                compute(u % D, buf);
+                load_w(u % D, min(kb + D, HB - 1));
+                __syncthreads();
             }
-            compute(u % D, buf);
-            load_w(u % D, min(kb + D, HB - 1));
-            __syncthreads();
         }
-    }
+    };
+    if (__builtin_amdgcn_readfirstlane(erows) <= BM) body(BoolC<true>{});
+    else body(BoolC<false>{});
 
 #pragma unroll
     for (int m = 0; m < MTW; ++m) {
@@ -315,12 +329,8 @@ hipError_t launch_gemm1_wide(const Plan& p, const uint8_t* hs, const float* hs_s
     // three waves per SIMD. Measured against 32-, 96- and 128-row tiles and
     // 4- to 8-deep rings, more resident waves beat deeper rings here.
     dim3 grid(I / WIDE_G, max_mtiles(p.T, WIDE_BM));
-    if (wt_nt(p.T, WIDE_BM))
-        hipLaunchKernelGGL((gemm1_wide_kernel<WIDE_BM / 16, 2, 1, false, true>), grid, dim3(64 * WIDE_NW),
-                           0, s, p, hs, hs_scale, w1, w1s, 0);
-    else
-        hipLaunchKernelGGL((gemm1_wide_kernel<WIDE_BM / 16, 2, 1, false, false>), grid,
-                           dim3(64 * WIDE_NW), 0, s, p, hs, hs_scale, w1, w1s, 0);
+    hipLaunchKernelGGL((gemm1_wide_kernel<WIDE_BM / 16, 2, 1, false>), grid, dim3(64 * WIDE_NW), 0, s,
+                       p, hs, hs_scale, w1, w1s, 0);
     return hipGetLastError();
 }
 
@@ -334,12 +344,8 @@ hipError_t launch_gemm1_wide_sorting(const Plan& p, const uint8_t* hs, const flo
     if (p.T <= 0) return hipSuccess;
     if (p.T > WIDE_SORT_MAX_T) return hipErrorInvalidValue;
     dim3 grid(I / WIDE_G, max_mtiles(p.T, WIDE_BM));
-    if (wt_nt(p.T, WIDE_BM))
-        hipLaunchKernelGGL((gemm1_wide_kernel<WIDE_BM / 16, 2, 1, true, true>), grid, dim3(64 * WIDE_NW),
-                           0, s, p, hs, hs_scale, w1, w1s, bm2);
-    else
-        hipLaunchKernelGGL((gemm1_wide_kernel<WIDE_BM / 16, 2, 1, true, false>), grid,
-                           dim3(64 * WIDE_NW), 0, s, p, hs, hs_scale, w1, w1s, bm2);
+    hipLaunchKernelGGL((gemm1_wide_kernel<WIDE_BM / 16, 2, 1, true>), grid, dim3(64 * WIDE_NW), 0, s,
+                       p, hs, hs_scale, w1, w1s, bm2);
     return hipGetLastError();
 }
 

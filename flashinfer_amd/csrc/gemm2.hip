@@ -70,7 +70,7 @@ __device__ __forceinline__ v4f mfma_block(const Frag16& a, const Frag16& al, con
     return acc;
 }
 
-template <int MT, int D, int NW, int NQ, int MODE, int KS, bool NT>
+template <int MT, int D, int NW, int NQ, int MODE, int KS>
 __global__ __launch_bounds__(64 * NW * KS) void gemm2_stream_kernel(
     Plan p, const uint8_t* __restrict__ w2, const float* __restrict__ w2s) {
     constexpr int KB = IB / KS;  // k-blocks per wave
@@ -109,64 +109,79 @@ __global__ __launch_bounds__(64 * NW * KS) void gemm2_stream_kernel(
     }
     const float* sb_ptr = w2s + ((size_t)e * HB + nb) * IB;
 
-    WRaw b[D][NQ];
-    Frag16 a[D][MT];
-    Frag16 al[D][MT];  // PREC only
     v4f acc[MT][NQ];
     const v4f zero = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int i = 0; i < MT; ++i)
 #pragma unroll
         for (int q = 0; q < NQ; ++q) acc[i][q] = zero;
+    float wrow[MT][4];  // routing weights of this lane's rows
 
-    auto compute = [&](int d, int kb) __attribute__((always_inline)) {
-        const float sb = sb_ptr[kb_first + kb];
+    // The k loop, with the weight load policy of the tile's expert (NT: non-
+    // temporal, when this is its only row tile). Against a policy per launch
+    // from T: T=160 GEMM2 68.4 against 74.3 us, level at T = 1 ... 128. The
+    // asm markers keep the compiler from merging the two copies' first and
+    // last instructions, which kept both copies' registers live (136 -> 244
+    // VGPRs for the 64-column waves; 156 with the markers).
+    auto body = [&](auto nt) __attribute__((always_inline)) {
+        constexpr bool NT = decltype(nt)::value;
+        asm volatile("; weight load policy %0 begin" ::"n"(NT ? 1 : 0));
+        WRaw b[D][NQ];
+        Frag16 a[D][MT];
+        Frag16 al[D][MT];  // PREC only
+
+        auto compute = [&](int d, int kb) __attribute__((always_inline)) {
+            const float sb = sb_ptr[kb_first + kb];
 #pragma unroll
-        for (int i = 0; i < MT; ++i) {
+            for (int i = 0; i < MT; ++i) {
 #pragma unroll
-            for (int q = 0; q < NQ; ++q) {
-                const v4f pr = mfma_block<PREC>(a[d][i], al[d][i], wl_frag(b[d][q]));
-                acc[i][q][0] += pr[0] * sb;
-                acc[i][q][1] += pr[1] * sb;
-                acc[i][q][2] += pr[2] * sb;
-                acc[i][q][3] += pr[3] * sb;
+                for (int q = 0; q < NQ; ++q) {
+                    const v4f pr = mfma_block<PREC>(a[d][i], al[d][i], wl_frag(b[d][q]));
+                    acc[i][q][0] += pr[0] * sb;
+                    acc[i][q][1] += pr[1] * sb;
+                    acc[i][q][2] += pr[2] * sb;
+                    acc[i][q][3] += pr[3] * sb;
+                }
+            }
+        };
+        auto load = [&](int d, int kb) __attribute__((always_inline)) {
+#pragma unroll
+            for (int q = 0; q < NQ; ++q) b[d][q] = ld_wraw<NT>(wr, b_off[q] + (kb_first + kb) * BLK, 8 * I);
+#pragma unroll
+            for (int i = 0; i < MT; ++i) {
+                a[d][i] = ld_act(a_row[i], kb_first + kb, g);
+                if constexpr (PREC) al[d][i] = ld_act(al_row[i], kb_first + kb, g);
+            }
+        };
+
+#pragma unroll
+        for (int d = 0; d < D; ++d) load(d, d);
+#pragma unroll 1
+        for (int kb0 = 0; kb0 < KB - D; kb0 += D) {
+#pragma unroll
+            for (int d = 0; d < D; ++d) {
+                compute(d, kb0 + d);
+                load(d, kb0 + d + D);
             }
         }
+        // Routing weights of this lane's rows, loaded while the last D k-blocks
+        // are consumed (the asm below keeps them from being sunk into the
+        // per-row stores, where each would wait on its own load).
+#pragma unroll
+        for (int i = 0; i < MT; ++i)
+#pragma unroll
+            for (int rr = 0; rr < 4; ++rr) wrow[i][rr] = p.sorted_w[row0 + min(i * 16 + g * 4 + rr, nrows - 1)];
+#pragma unroll
+        for (int d = 0; d < D; ++d) compute(d, KB - D + d);
+#pragma unroll
+        for (int i = 0; i < MT; ++i)
+#pragma unroll
+            for (int rr = 0; rr < 4; ++rr) asm volatile("" : "+v"(wrow[i][rr]));
+        asm volatile("; weight load policy %0 end" ::"n"(NT ? 1 : 0));
     };
-    auto load = [&](int d, int kb) __attribute__((always_inline)) {
-#pragma unroll
-        for (int q = 0; q < NQ; ++q) b[d][q] = ld_wraw<NT>(wr, b_off[q] + (kb_first + kb) * BLK, 8 * I);
-#pragma unroll
-        for (int i = 0; i < MT; ++i) {
-            a[d][i] = ld_act(a_row[i], kb_first + kb, g);
-            if constexpr (PREC) al[d][i] = ld_act(al_row[i], kb_first + kb, g);
-        }
-    };
-
-#pragma unroll
-    for (int d = 0; d < D; ++d) load(d, d);
-#pragma unroll 1
-    for (int kb0 = 0; kb0 < KB - D; kb0 += D) {
-#pragma unroll
-        for (int d = 0; d < D; ++d) {
-            compute(d, kb0 + d);
-            load(d, kb0 + d + D);
-        }
-    }
-    // Routing weights of this lane's rows, loaded while the last D k-blocks
-    // are consumed (the asm below keeps them from being sunk into the
-    // per-row stores, where each would wait on its own load).
-    float wrow[MT][4];
-#pragma unroll
-    for (int i = 0; i < MT; ++i)
-#pragma unroll
-        for (int rr = 0; rr < 4; ++rr) wrow[i][rr] = p.sorted_w[row0 + min(i * 16 + g * 4 + rr, nrows - 1)];
-#pragma unroll
-    for (int d = 0; d < D; ++d) compute(d, KB - D + d);
-#pragma unroll
-    for (int i = 0; i < MT; ++i)
-#pragma unroll
-        for (int rr = 0; rr < 4; ++rr) asm volatile("" : "+v"(wrow[i][rr]));
+    const int erows = p.meta[META_EXPERT_OFF + e + 1] - p.meta[META_EXPERT_OFF + e];
+    if (__builtin_amdgcn_readfirstlane(erows) <= BM) body(BoolC<true>{});
+    else body(BoolC<false>{});
 
     // K split: the other waves of the column group hand their partial sums to
     // the first through LDS, which adds them in split order.
@@ -231,12 +246,7 @@ int gemm2_bm(int variant) {
 template <int MT, int D, int NW, int NQ, int MODE, int KS>
 static void launch_stream2_mode(const Plan& p, const uint8_t* w2, const float* w2s, dim3 grid,
                                 dim3 block, hipStream_t s) {
-    if (wt_nt(p.T, 16 * MT))
-        hipLaunchKernelGGL((gemm2_stream_kernel<MT, D, NW, NQ, MODE, KS, true>), grid, block, 0, s, p, w2,
-                           w2s);
-    else
-        hipLaunchKernelGGL((gemm2_stream_kernel<MT, D, NW, NQ, MODE, KS, false>), grid, block, 0, s, p, w2,
-                           w2s);
+    hipLaunchKernelGGL((gemm2_stream_kernel<MT, D, NW, NQ, MODE, KS>), grid, block, 0, s, p, w2, w2s);
 }
 
 template <int MT, int D, int NW, int NQ, int KS = 1>
