@@ -5,14 +5,18 @@
 //   part[s, n] = bf16(w_s * sum_kb sb2[e, n/128, kb] * (act[s, kb-block] . W2[e, n, kb-block]))
 // with bf16 activations and fp8 weights widened to bf16 (exact).
 //
-// Shape (template <MTW, D, DA, MODE>): a workgroup of 4 waves owns BM = 16*MTW
-// slots of one expert and 64 output columns; wave w owns columns n0..n0+15
+// Shape (template <MTW, D, DA, MODE>): a workgroup of 8 waves owns BM = 16*MTW
+// slots of one expert and 128 output columns; wave w owns columns n0..n0+15
 // for all BM rows, so its 16 weight rows go global -> VGPR through a D-deep
 // register ring (no two waves share them). The BM activation rows of a
 // k-block (contiguous slots, 256 bytes each) are loaded once per workgroup
 // into a DA-deep register staging ring and written to an LDS double buffer
-// one k-block ahead of their use: one barrier per k-block. The 64 columns lie
-// in one 128-column scale block, so sb2 is one uniform value per k-block.
+// one k-block ahead of their use: one barrier per k-block. The 128 columns are
+// one 128-column scale block, so sb2 is one uniform value per k-block. Every
+// column group re-reads the tile's activation rows from L2 (as many bytes as
+// the weights at T=256 with 64-column groups); 128 columns halve that: 72.7
+// against 77.0 us at T=256, 136.5 against 154.9 with every token on the same
+// 8 experts.
 // MODE (G2_*): rows go to part (bf16) or part_f32; with G2_SPLIT the act_lo
 // rows ride along as rows BM..2BM-1 of the LDS buffers and each k step runs
 // the MFMAs of both halves against the same bf16 weights.
@@ -29,7 +33,7 @@ namespace mimoe {
 namespace {
 constexpr int gcd2(int a, int b) { return b == 0 ? a : gcd2(b, a % b); }
 constexpr int lcm2(int a, int b) { return a / gcd2(a, b) * b; }
-constexpr int W2_NW = 4;           // waves per workgroup
+constexpr int W2_NW = 8;           // waves per workgroup
 constexpr int W2_N = 16 * W2_NW;   // output columns per workgroup
 constexpr int W2_BM = 32;          // rows per workgroup (see the launcher)
 }  // namespace
@@ -199,9 +203,10 @@ __global__ __launch_bounds__(64 * W2_NW) void gemm2_wide_kernel(Plan p, const ui
 }
 
 hipError_t launch_gemm2_wide(const Plan& p, const uint8_t* w2, const float* w2s, hipStream_t s) {
-    // 32 rows, weights 2 k-blocks ahead, activations 1 ahead: 80 VGPRs and
-    // 17 KB of LDS, so six workgroups per CU. Measured against 64- and
-    // 128-row tiles and 4- and 8-deep rings.
+    // 32 rows x 128 columns, weights 2 k-blocks ahead, activations 1 ahead:
+    // 74 VGPRs and 18 KB of LDS, so three 8-wave workgroups per CU. Measured
+    // against 64- and 128-row tiles, 64-column workgroups and 4- and 8-deep
+    // rings.
     dim3 grid(H / W2_N, max_mtiles(p.T, W2_BM));
     constexpr int MTW = W2_BM / 16;
     switch (gemm2_mode(p)) {
