@@ -271,7 +271,12 @@ Variants pick_variants(int64_t T) {
     else if (T <= 176) v = {15, 13};  // wide GEMM2 ahead by 3.5 us at T = 192, behind by ~2 at 160
     else if (T <= 256) v = {15, 15};
     else if (T <= 1536) v = {15, 3};
-    else v = {18, 3};  // GEMM1 tile with swapped operands, pipelined scale FMAs (4-6% over 3)
+    // GEMM1 LDS tile as one software pipeline (barriers inside the MFMA
+    // stream, weight fragments held in registers): bitwise equal to variant
+    // 18 and faster at every T (GEMM1 per launch, one process: T=8192 401-420
+    // against 436-509 us, T=14000 skewed 2972 against 3151, T=3072 287
+    // against 308); level with the wide kernel at T=2048.
+    else v = {19, 3};
     const char* env = getenv("MI_MOE_VARIANT");
     if (env && *env) {
         int a = -1, b = -1;

@@ -393,10 +393,12 @@ hipError_t launch_gemm2_wide(const Plan& p, const uint8_t* w2, const float* w2s,
 // columns per wave), 17 GEMM2 fused with the combine
 // with K split over its 4 waves, 18 the GEMM1 LDS tile of variant 3 with the MFMA
 // operands swapped (one scale factor per lane and tile) and the scale FMAs
-// software-pipelined behind later MFMAs (for GEMM2, the tile of variant 3).
-// An id without a kernel of its own in one GEMM (9, 10 and 17 for GEMM1)
-// runs that GEMM's default stream shape.
-constexpr int NUM_VARIANTS = 19;
+// software-pipelined behind later MFMAs (for GEMM2, the tile of variant 3),
+// 19 the GEMM1 LDS tile whose waves hold a k-block's weight fragments in
+// registers so that each weight copy has two k-blocks to arrive.
+// An id without a kernel of its own in one GEMM (9, 10 and 17 for GEMM1, 19
+// for GEMM2) runs that GEMM's default stream shape.
+constexpr int NUM_VARIANTS = 20;
 // GEMM2 variants that also perform the combine (decode sizes only): tiles
 // dealt to the 4 waves, or k-blocks split over them.
 constexpr int VARIANT_GEMM2_COMBINE = 10;

@@ -230,6 +230,7 @@ int gemm1_bm(int variant) {
         case 3: return 256;
         case 4: return 128;
         case 18: return 256;
+        case 19: return 256;
         case 11: return 32;
         case 12: return 32;
         case 15: return 64;
@@ -279,7 +280,7 @@ hipError_t launch_gemm1_front(const Plan& p, const uint8_t* hs, const float* hs_
 hipError_t launch_gemm1(const Plan& p, const uint8_t* hs, const float* hs_scale, const uint8_t* w1,
                         const float* w1s, int variant, hipStream_t s) {
     if (p.T <= 0) return hipSuccess;
-    if ((variant >= 3 && variant <= 4) || variant == 18)
+    if ((variant >= 3 && variant <= 4) || variant == 18 || variant == 19)
         return launch_gemm1_tile(p, hs, hs_scale, w1, w1s, variant, s);
     if (variant == 15) return launch_gemm1_wide(p, hs, hs_scale, w1, w1s, s);
     switch (variant) {

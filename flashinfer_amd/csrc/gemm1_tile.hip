@@ -394,9 +394,264 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm1_tile_t_kernel(
     }
 }
 
+// The same 256 x (128 + 128) tile as one software pipeline (variant 19).
+//
+// The 8 waves form 2 row groups x 4 column groups: wave (wm, wn) owns rows
+// 128wm .. 128wm+127 (8 row tiles of 16) and gate columns 32wn .. 32wn+31
+// (2 column tiles) plus the matching up columns, 32 MFMAs per k-block as in
+// variants 3 and 18. A wave keeps its four weight fragments of a k-block in
+// registers (32 VGPRs) and streams the 8 activation fragments from LDS. The
+// two barriers of a k-block sit inside the MFMA stream, so no wave waits on
+// LDS or on a barrier with an empty matrix core queue:
+//   * barrier X, after row tile 0: every wave has its weight fragments of
+//     k-block kb in registers (read during k-block kb-1), so that stage's
+//     weight region is free and the copy of the weights of k-block kb+2 goes
+//     there: a weight copy has ~1.75 k-blocks to arrive;
+//   * barrier Y, before row tile 7: the copies of k-block kb+1 have landed
+//     (vmcnt leaves only the weights of kb+2 outstanding), and every wave has
+//     read its last activation fragment of kb, so the activation rows of
+//     k-block kb+2 are copied into this stage's activation region (one
+//     k-block to arrive). During row tile 7 each wave reads the next
+//     k-block's weight fragments into the same registers right after their
+//     last MFMA, its first activation fragment and its row scales.
+// Weights are the operand that comes from HBM (an expert's column tile is
+// read by its few row tiles, an activation row tile by all 16 column tiles).
+// MFMA operands are swapped as in variant 18 (weights are the A operand, so
+// a lane holds four output columns of one row and one scale factor per
+// tile), and each MFMA's four scale FMAs issue after the MFMA four later
+// (the next row tile's, same column tile); the last row tile's carry into
+// the next k-block.
+struct G1W {
+    static constexpr int NW = 8;
+    static constexpr int THREADS = 64 * NW;
+    static constexpr int BM = 256;
+    static constexpr int BG = 128;
+    static constexpr int NT = I / BG;
+    static constexpr int A_BYTES = BM * BLK;
+    static constexpr int B_BYTES = 2 * BG * BLK;
+    static constexpr int SA_BYTES = BM * 4;
+    static constexpr int STAGE = A_BYTES + B_BYTES + SA_BYTES;
+    static constexpr int A_LD = A_BYTES / 1024 / NW;
+    static constexpr int B_LD = B_BYTES / 1024 / NW;
+    static_assert(A_LD == 4 && B_LD == 4, "loader split: vmcnt(4) leaves one k-block of weight copies");
+    static_assert(2 * STAGE + 2 * 64 * 4 <= 160 * 1024, "LDS budget");
+    static_assert(HB <= 64 && HB >= 2, "weight scales: one lane per k-block");
+};
+
+template <int GM>
+__global__ __launch_bounds__(512) void gemm1_tile_w_kernel(
+    Plan p, const uint8_t* __restrict__ hs, const float* __restrict__ hs_scale,
+    const uint8_t* __restrict__ w1, const float* __restrict__ w1s) {
+    using C = G1W;
+    __shared__ __attribute__((aligned(1024))) uint8_t smem[2 * C::STAGE];
+    __shared__ __attribute__((aligned(16))) float s_sb[2 * 64];  // [gate | up][kb] weight scales
+
+    int e, row0, nrows, nt;
+    if (!tile_coords<C::NT, GM>(p.meta, META_MTILE1, C::BM, e, row0, nrows, nt)) return;
+    // wave-uniform by construction; kept in SGPRs for the copies' scalar bases
+    e = __builtin_amdgcn_readfirstlane(e);
+    nt = __builtin_amdgcn_readfirstlane(nt);
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int jb = nt * C::BG;
+
+    uint32_t a_off[C::A_LD], b_off[C::B_LD];
+#pragma unroll
+    for (int i = 0; i < C::A_LD; ++i) {
+        const int row = 8 * (wave * C::A_LD + i) + (lane >> 3);
+        const int c = (lane & 7) ^ swzq(row);
+        const int tok = p.sorted_tok[row0 + min(row, nrows - 1)];
+        a_off[i] = (uint32_t)tok * H + c * 16;
+    }
+#pragma unroll
+    for (int i = 0; i < C::B_LD; ++i) {
+        const int row = 8 * (wave * C::B_LD + i) + (lane >> 3);
+        const int c = (lane & 7) ^ swzq(row);
+        const int wrow = row < C::BG ? jb + row : I + jb + (row - C::BG);
+        b_off[i] = (uint32_t)((e * N1 + wrow) * H + c * 16);
+    }
+    // Activation scales sit in LDS as [row group wm][r][m] (row 128wm + 16m
+    // + r), so a lane reads the scales of its 8 rows as two 16-byte vectors.
+    // Waves 0..3 copy 64 of them each; lane l of wave w takes index 64w + l.
+    uint32_t sa_off = 0;
+    if (wave < 4) {
+        const int idx = 64 * wave + lane;
+        const int row = 128 * (idx >> 7) + 16 * (idx & 7) + ((idx & 127) >> 3);
+        sa_off = (uint32_t)p.sorted_tok[row0 + min(row, nrows - 1)];
+    }
+
+    // copies address their rows as a k-block base (SGPRs) + a 32-bit offset
+    auto issue_a = [&](int stage, int kb) __attribute__((always_inline)) {
+        uint8_t* s = smem + stage * C::STAGE;
+        const uint8_t* base = hs + kb * BLK;
+#pragma unroll
+        for (int i = 0; i < C::A_LD; ++i) g2l16s(base, a_off[i], s + (wave * C::A_LD + i) * 1024);
+        if (wave < 4) g2l4s(hs_scale + (size_t)kb * p.T, sa_off * 4, s + C::A_BYTES + C::B_BYTES + wave * 256);
+    };
+    auto issue_b = [&](int stage, int kb) __attribute__((always_inline)) {
+        uint8_t* s = smem + stage * C::STAGE + C::A_BYTES;
+        const uint8_t* base = w1 + kb * BLK;
+#pragma unroll
+        for (int i = 0; i < C::B_LD; ++i) g2l16s(base, b_off[i], s + (wave * C::B_LD + i) * 1024);
+    };
+
+    // The tile's weight scales (one 128-column block of gate, one of up, for
+    // every k-block) are copied once by waves 4 and 5.
+    if (wave == 4 || wave == 5) {
+        const int nb = wave == 4 ? jb / BLK : (I + jb) / BLK;
+        if (lane < HB) g2l4s(w1s + ((size_t)e * N1B + nb) * HB, lane * 4, s_sb + (wave - 4) * 64);
+    }
+    // Prologue, in the order of the steady state: weights and activations of
+    // k-block 0, weights of 1; then (after the barrier that plays barrier Y
+    // of k-block -1) activations of 1.
+    issue_b(0, 0);
+    issue_a(0, 0);
+    issue_b(1, 1);
+    asm volatile("s_waitcnt vmcnt(4)\n\ts_barrier" ::: "memory");
+    issue_a(1, 1);
+
+    const int wn = wave & 3, wm = wave >> 2;
+    const int r = lane & 15, g = lane >> 4;
+    const bool active = wm * 128 < nrows;  // wave-uniform: rows past the expert only copy
+
+    auto frag = [&](const uint8_t* s, int row) __attribute__((always_inline)) {
+        const uint8_t* base = s + row * BLK;
+        const int sw = swzq(row);
+        const v4i lo = lds16(base + ((g ^ sw) << 4));
+        const v4i hi = lds16(base + (((g + 4) ^ sw) << 4));
+        return (v8i){lo.x, lo.y, lo.z, lo.w, hi.x, hi.y, hi.z, hi.w};
+    };
+    auto brow = [&](int n) __attribute__((always_inline)) {
+        return n < 2 ? 32 * wn + 16 * n + r : C::BG + 32 * wn + 16 * (n - 2) + r;
+    };
+
+    if (!active) {
+        // Rows past the expert: copies and barriers only, in step with the
+        // other waves (two barriers per k-block).
+#pragma unroll 1
+        for (int kb = 0; kb < HB; ++kb) {
+            const int kb2 = min(kb + 2, HB - 1);
+            asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+            issue_b(kb & 1, kb2);
+            asm volatile("s_waitcnt vmcnt(4) lgkmcnt(0)\n\ts_barrier" ::: "memory");
+            issue_a(kb & 1, kb2);
+        }
+        wait_vmem();  // no copy into LDS may be pending when the workgroup ends
+        return;
+    }
+
+    // this lane's 8 row scales (rows 128wm + 16m + r) and the weight scales
+    // of k-block kb (stage s)
+    float sa[8], sbg, sbu;
+    auto scales = [&](const uint8_t* s, int kb) __attribute__((always_inline)) {
+        const float* sSA = reinterpret_cast<const float*>(s + C::A_BYTES + C::B_BYTES);
+        const float4 s0 = *reinterpret_cast<const float4*>(sSA + wm * 128 + r * 8);
+        const float4 s1 = *reinterpret_cast<const float4*>(sSA + wm * 128 + r * 8 + 4);
+        sa[0] = s0.x; sa[1] = s0.y; sa[2] = s0.z; sa[3] = s0.w;
+        sa[4] = s1.x; sa[5] = s1.y; sa[6] = s1.z; sa[7] = s1.w;
+        sbg = s_sb[kb];
+        sbu = s_sb[64 + kb];
+    };
+
+    v4f acc[8][4];  // [row tile m][column tile n: 0, 1 gate; 2, 3 up]
+    const v4f zero = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int m = 0; m < 8; ++m)
+#pragma unroll
+        for (int n = 0; n < 4; ++n) acc[m][n] = zero;
+    v8i bfr[4], acur, anext;
+#pragma unroll
+    for (int n = 0; n < 4; ++n) bfr[n] = frag(smem + C::A_BYTES, brow(n));
+    acur = frag(smem, wm * 128 + r);
+    scales(smem, 0);
+
+    // The k-loop is straight-line code: the copies of the last two k-blocks
+    // repeat k-block HB-1 into regions no wave reads again, and the
+    // fragments and scales read for "k-block HB" are never used.
+#pragma unroll 1
+    for (int kb = 0; kb < HB; ++kb) {
+        const int cur = kb & 1;
+        uint8_t* const sc = smem + cur * C::STAGE;        // this k-block's stage
+        uint8_t* const sn = smem + (cur ^ 1) * C::STAGE;  // the next one's
+        const int kb1 = min(kb + 1, HB - 1), kb2 = min(kb + 2, HB - 1);
+        // scale-and-accumulate of MFMA result x (row tile tm, column tile tn)
+        auto fma4 = [&](const v4f& x, int tm, int tn) __attribute__((always_inline)) {
+            const float u = sa[tm] * (tn < 2 ? sbg : sbu);
+#pragma unroll
+            for (int v = 0; v < 4; ++v) acc[tm][tn][v] += x[v] * u;
+        };
+        // The compiler would sink the MFMAs and FMAs below the barriers (they
+        // touch no memory) and hoist all fragment reads to the top, keeping
+        // every fragment live at once: empty asm statements naming the
+        // accumulators pin the arithmetic before each barrier, and a
+        // compiler-only memory fence per row tile keeps each activation
+        // fragment read one row tile ahead.
+        auto pin_rows = [&](int m0, int m1) __attribute__((always_inline)) {
+#pragma unroll
+            for (int m = m0; m < m1; ++m)
+                asm volatile("" : "+v"(acc[m][0]), "+v"(acc[m][1]), "+v"(acc[m][2]), "+v"(acc[m][3]));
+        };
+        v4f pr[32];
+#pragma unroll
+        for (int t = 0; t < 32; ++t) {
+            const int m = t >> 2, n = t & 3;
+            if (n == 0) asm volatile("" ::: "memory");
+            if (t == 4) {  // barrier X: weight fragments of kb are in registers everywhere
+                pin_rows(6, 8);
+                asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+                issue_b(cur, kb2);
+            }
+            if (t == 28) {  // barrier Y: k-block kb+1 has landed; activations of kb all read
+                pin_rows(0, 6);
+                asm volatile("s_waitcnt vmcnt(4) lgkmcnt(0)\n\ts_barrier" ::: "memory");
+                issue_a(cur, kb2);
+                anext = frag(sn, wm * 128 + r);
+            }
+            if (n == 0 && m < 7) anext = frag(sc, wm * 128 + 16 * (m + 1) + r);
+            pr[t] = mfma_f8_16x16x128(bfr[n], acur, zero);
+            if (m == 7) bfr[n] = frag(sn + C::A_BYTES, brow(n));
+            if (n == 3) acur = anext;
+            if (t >= 4) fma4(pr[t - 4], (t - 4) >> 2, (t - 4) & 3);
+            __builtin_amdgcn_sched_barrier(0);
+        }
+#pragma unroll
+        for (int n = 0; n < 4; ++n) fma4(pr[28 + n], 7, n);
+        scales(sn, kb1);
+    }
+    wait_vmem();  // no copy into LDS may be pending when the workgroup ends
+
+#pragma unroll
+    for (int m = 0; m < 8; ++m) {
+        const int row = wm * 128 + m * 16 + r;
+        if (row < nrows) {
+#pragma unroll
+            for (int n = 0; n < 2; ++n) {
+                uint32_t w[2], wl[2];
+#pragma unroll
+                for (int h = 0; h < 2; ++h) {
+                    const float v0 = silu(acc[m][n + 2][2 * h]) * acc[m][n][2 * h];
+                    const float v1 = silu(acc[m][n + 2][2 * h + 1]) * acc[m][n][2 * h + 1];
+                    const uint16_t h0 = f2bf(v0), h1 = f2bf(v1);
+                    w[h] = (uint32_t)h0 | ((uint32_t)h1 << 16);
+                    wl[h] = (uint32_t)f2bf(v0 - bf2f(h0)) | ((uint32_t)f2bf(v1 - bf2f(h1)) << 16);
+                }
+                const size_t idx = (size_t)(row0 + row) * I + jb + wn * 32 + n * 16 + 4 * g;
+                *reinterpret_cast<uint2*>(p.act + idx) = make_uint2(w[0], w[1]);
+                if (p.act_lo) *reinterpret_cast<uint2*>(p.act_lo + idx) = make_uint2(wl[0], wl[1]);
+            }
+        }
+    }
+}
+
 hipError_t launch_gemm1_tile(const Plan& p, const uint8_t* hs, const float* hs_scale,
                              const uint8_t* w1, const float* w1s, int variant, hipStream_t s) {
-    if (variant == 18) {
+    if (variant == 19) {
+        const int tiles = max_mtiles(p.T, G1W::BM) * G1W::NT;
+        hipLaunchKernelGGL((gemm1_tile_w_kernel<16>), dim3((tiles + 7) / 8 * 8), dim3(G1W::THREADS), 0,
+                           s, p, hs, hs_scale, w1, w1s);
+    } else if (variant == 18) {
         using C = G1Tile<4, 2>;
         const int tiles = max_mtiles(p.T, C::BM) * C::NT;
         hipLaunchKernelGGL((gemm1_tile_t_kernel<4, 2, 16>), dim3((tiles + 7) / 8 * 8),

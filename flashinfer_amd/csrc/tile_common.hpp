@@ -35,6 +35,23 @@ __device__ __forceinline__ void g2l4(const void* gsrc, void* lds_base) {
                  : "memory", "m0");
 }
 
+// The same two copies with a wave-uniform 64-bit base in SGPRs and a 32-bit
+// per-lane byte offset (the saddr form: address = sbase + voff): one VGPR per
+// copy instead of a 64-bit address per lane.
+__device__ __forceinline__ void g2l16s(const void* sbase, uint32_t voff, void* lds_base) {
+    asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, %1"
+                 :
+                 : "v"(voff), "s"(sbase), "s"(lds_addr(lds_base))
+                 : "memory", "m0");
+}
+
+__device__ __forceinline__ void g2l4s(const void* sbase, uint32_t voff, void* lds_base) {
+    asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dword %0, %1"
+                 :
+                 : "v"(voff), "s"(sbase), "s"(lds_addr(lds_base))
+                 : "memory", "m0");
+}
+
 __device__ __forceinline__ void wait_vmem() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
 
 // XOR swizzle of the 16-byte chunk index inside a 128-byte LDS row: 16
