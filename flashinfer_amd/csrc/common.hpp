@@ -232,6 +232,10 @@ template <bool B>
 struct BoolC {
     static constexpr bool value = B;
 };
+template <int V>
+struct IntC {
+    static constexpr int value = V;
+};
 
 __device__ __forceinline__ v8i wl_frag(const WRaw& w) {
     constexpr int ROR8 = 0x128;  // DPP row_ror:8

@@ -542,107 +542,131 @@ __global__ __launch_bounds__(512) void gemm1_tile_w_kernel(
         return;
     }
 
-    // this lane's 8 row scales (rows 128wm + 16m + r) and the weight scales
-    // of k-block kb (stage s)
-    float sa[8], sbg, sbu;
-    auto scales = [&](const uint8_t* s, int kb) __attribute__((always_inline)) {
-        const float* sSA = reinterpret_cast<const float*>(s + C::A_BYTES + C::B_BYTES);
-        const float4 s0 = *reinterpret_cast<const float4*>(sSA + wm * 128 + r * 8);
-        const float4 s1 = *reinterpret_cast<const float4*>(sSA + wm * 128 + r * 8 + 4);
-        sa[0] = s0.x; sa[1] = s0.y; sa[2] = s0.z; sa[3] = s0.w;
-        sa[4] = s1.x; sa[5] = s1.y; sa[6] = s1.z; sa[7] = s1.w;
-        sbg = s_sb[kb];
-        sbu = s_sb[64 + kb];
-    };
+    // The arithmetic of one wave with MT row tiles (8, or 4 when the wave's
+    // rows past 64 lie beyond the expert: partial row tiles at the end of an
+    // expert then cost half the MFMAs). Both forms run the same copies and
+    // barriers.
+    auto compute = [&](auto mt_c) __attribute__((always_inline)) {
+        constexpr int MT = decltype(mt_c)::value;
+        static_assert(MT >= 3 && MT <= 8, "barrier X after row tile 0, Y before the last");
+        constexpr int NTT = 4 * MT;        // MFMAs per k-block
+        constexpr int TY = 4 * (MT - 1);   // barrier Y before the last row tile
+        // scale factors sa * sb of this lane's rows (128wm + 16m + r) for the
+        // gate and up column blocks of k-block kb (stage s)
+        float ug[MT], uu[MT];
+        auto scales = [&](const uint8_t* s, int kb) __attribute__((always_inline)) {
+            const float* sSA = reinterpret_cast<const float*>(s + C::A_BYTES + C::B_BYTES);
+            const float4 s0 = *reinterpret_cast<const float4*>(sSA + wm * 128 + r * 8);
+            const float4 s1 = *reinterpret_cast<const float4*>(sSA + wm * 128 + r * 8 + 4);
+            const float sa[8] = {s0.x, s0.y, s0.z, s0.w, s1.x, s1.y, s1.z, s1.w};
+            const float sbg = s_sb[kb], sbu = s_sb[64 + kb];
+#pragma unroll
+            for (int m = 0; m < MT; ++m) { ug[m] = sa[m] * sbg; uu[m] = sa[m] * sbu; }
+        };
 
-    v4f acc[8][4];  // [row tile m][column tile n: 0, 1 gate; 2, 3 up]
-    const v4f zero = {0.f, 0.f, 0.f, 0.f};
+        v4f acc[MT][4];  // [row tile m][column tile n: 0, 1 gate; 2, 3 up]
+        const v4f zero = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-    for (int m = 0; m < 8; ++m)
+        for (int m = 0; m < MT; ++m)
 #pragma unroll
-        for (int n = 0; n < 4; ++n) acc[m][n] = zero;
-    v8i bfr[4], acur, anext;
+            for (int n = 0; n < 4; ++n) acc[m][n] = zero;
+        // weight fragments of the k-block; activation fragments of the current
+        // row tile and the next two (each read two row tiles ahead of its
+        // MFMAs: one row tile of MFMAs is shorter than an LDS read under load)
+        v8i bfr[4], acur, anx1, anx2;
 #pragma unroll
-    for (int n = 0; n < 4; ++n) bfr[n] = frag(smem + C::A_BYTES, brow(n));
-    acur = frag(smem, wm * 128 + r);
-    scales(smem, 0);
+        for (int n = 0; n < 4; ++n) bfr[n] = frag(smem + C::A_BYTES, brow(n));
+        acur = frag(smem, wm * 128 + r);
+        anx1 = frag(smem, wm * 128 + 16 + r);
+        scales(smem, 0);
 
-    // The k-loop is straight-line code: the copies of the last two k-blocks
-    // repeat k-block HB-1 into regions no wave reads again, and the
-    // fragments and scales read for "k-block HB" are never used.
+        // The k-loop is straight-line code: the copies of the last two
+        // k-blocks repeat k-block HB-1 into regions no wave reads again, and
+        // the fragments and scales read for "k-block HB" are never used.
 #pragma unroll 1
-    for (int kb = 0; kb < HB; ++kb) {
-        const int cur = kb & 1;
-        uint8_t* const sc = smem + cur * C::STAGE;        // this k-block's stage
-        uint8_t* const sn = smem + (cur ^ 1) * C::STAGE;  // the next one's
-        const int kb1 = min(kb + 1, HB - 1), kb2 = min(kb + 2, HB - 1);
-        // scale-and-accumulate of MFMA result x (row tile tm, column tile tn)
-        auto fma4 = [&](const v4f& x, int tm, int tn) __attribute__((always_inline)) {
-            const float u = sa[tm] * (tn < 2 ? sbg : sbu);
+        for (int kb = 0; kb < HB; ++kb) {
+            const int cur = kb & 1;
+            uint8_t* const sc = smem + cur * C::STAGE;        // this k-block's stage
+            uint8_t* const sn = smem + (cur ^ 1) * C::STAGE;  // the next one's
+            const int kb1 = min(kb + 1, HB - 1), kb2 = min(kb + 2, HB - 1);
+            // scale-and-accumulate of MFMA result x (row tile tm, column tile tn)
+            auto fma4 = [&](const v4f& x, int tm, int tn) __attribute__((always_inline)) {
+                const float u = tn < 2 ? ug[tm] : uu[tm];
 #pragma unroll
-            for (int v = 0; v < 4; ++v) acc[tm][tn][v] += x[v] * u;
-        };
-        // The compiler would sink the MFMAs and FMAs below the barriers (they
-        // touch no memory) and hoist all fragment reads to the top, keeping
-        // every fragment live at once: empty asm statements naming the
-        // accumulators pin the arithmetic before each barrier, and a
-        // compiler-only memory fence per row tile keeps each activation
-        // fragment read one row tile ahead.
-        auto pin_rows = [&](int m0, int m1) __attribute__((always_inline)) {
+                for (int v = 0; v < 4; ++v) acc[tm][tn][v] += x[v] * u;
+            };
+            // The compiler would sink the MFMAs and FMAs below the barriers
+            // (they touch no memory) and hoist all fragment reads to the top,
+            // keeping every fragment live at once: empty asm statements naming
+            // the accumulators pin the arithmetic before each barrier, and a
+            // compiler-only memory fence per row tile keeps each activation
+            // fragment read in its row tile.
+            auto pin_rows = [&](int m0, int m1) __attribute__((always_inline)) {
 #pragma unroll
-            for (int m = m0; m < m1; ++m)
-                asm volatile("" : "+v"(acc[m][0]), "+v"(acc[m][1]), "+v"(acc[m][2]), "+v"(acc[m][3]));
-        };
-        v4f pr[32];
+                for (int m = m0; m < m1; ++m)
+                    asm volatile("" : "+v"(acc[m][0]), "+v"(acc[m][1]), "+v"(acc[m][2]), "+v"(acc[m][3]));
+            };
+            v4f pr[NTT];
 #pragma unroll
-        for (int t = 0; t < 32; ++t) {
-            const int m = t >> 2, n = t & 3;
-            if (n == 0) asm volatile("" ::: "memory");
-            if (t == 4) {  // barrier X: weight fragments of kb are in registers everywhere
-                pin_rows(6, 8);
-                asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
-                issue_b(cur, kb2);
+            for (int t = 0; t < NTT; ++t) {
+                const int m = t >> 2, n = t & 3;
+                if (n == 0) asm volatile("" ::: "memory");
+                if (t == 4) {  // barrier X: weight fragments of kb are in registers everywhere
+                    pin_rows(MT - 2, MT);
+                    asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+                    issue_b(cur, kb2);
+                }
+                if (t == TY) {  // barrier Y: k-block kb+1 has landed; activations of kb all read
+                    pin_rows(0, MT - 2);
+                    asm volatile("s_waitcnt vmcnt(4) lgkmcnt(0)\n\ts_barrier" ::: "memory");
+                    issue_a(cur, kb2);
+                }
+                // activation fragments two row tiles ahead: rows of kb while
+                // m < MT - 2; the first two row tiles of kb+1 once it has landed
+                if (n == 0 && m < MT - 2) anx2 = frag(sc, wm * 128 + 16 * (m + 2) + r);
+                if (t == TY) anx1 = frag(sn, wm * 128 + r);
+                if (t == TY + 1) anx2 = frag(sn, wm * 128 + 16 + r);
+                pr[t] = mfma_f8_16x16x128(bfr[n], acur, zero);
+                if (m == MT - 1) bfr[n] = frag(sn + C::A_BYTES, brow(n));
+                if (n == 3) {  // the next row tile's fragment becomes current
+                    acur = anx1;
+                    anx1 = anx2;
+                }
+                if (t >= 4) fma4(pr[t - 4], (t - 4) >> 2, (t - 4) & 3);
+                __builtin_amdgcn_sched_barrier(0);
             }
-            if (t == 28) {  // barrier Y: k-block kb+1 has landed; activations of kb all read
-                pin_rows(0, 6);
-                asm volatile("s_waitcnt vmcnt(4) lgkmcnt(0)\n\ts_barrier" ::: "memory");
-                issue_a(cur, kb2);
-                anext = frag(sn, wm * 128 + r);
-            }
-            if (n == 0 && m < 7) anext = frag(sc, wm * 128 + 16 * (m + 1) + r);
-            pr[t] = mfma_f8_16x16x128(bfr[n], acur, zero);
-            if (m == 7) bfr[n] = frag(sn + C::A_BYTES, brow(n));
-            if (n == 3) acur = anext;
-            if (t >= 4) fma4(pr[t - 4], (t - 4) >> 2, (t - 4) & 3);
-            __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+            for (int n = 0; n < 4; ++n) fma4(pr[NTT - 4 + n], MT - 1, n);
+            scales(sn, kb1);
         }
-#pragma unroll
-        for (int n = 0; n < 4; ++n) fma4(pr[28 + n], 7, n);
-        scales(sn, kb1);
-    }
-    wait_vmem();  // no copy into LDS may be pending when the workgroup ends
+        wait_vmem();  // no copy into LDS may be pending when the workgroup ends
 
 #pragma unroll
-    for (int m = 0; m < 8; ++m) {
-        const int row = wm * 128 + m * 16 + r;
-        if (row < nrows) {
+        for (int m = 0; m < MT; ++m) {
+            const int row = wm * 128 + m * 16 + r;
+            if (row < nrows) {
 #pragma unroll
-            for (int n = 0; n < 2; ++n) {
-                uint32_t w[2], wl[2];
+                for (int n = 0; n < 2; ++n) {
+                    uint32_t w[2], wl[2];
 #pragma unroll
-                for (int h = 0; h < 2; ++h) {
-                    const float v0 = silu(acc[m][n + 2][2 * h]) * acc[m][n][2 * h];
-                    const float v1 = silu(acc[m][n + 2][2 * h + 1]) * acc[m][n][2 * h + 1];
-                    const uint16_t h0 = f2bf(v0), h1 = f2bf(v1);
-                    w[h] = (uint32_t)h0 | ((uint32_t)h1 << 16);
-                    wl[h] = (uint32_t)f2bf(v0 - bf2f(h0)) | ((uint32_t)f2bf(v1 - bf2f(h1)) << 16);
+                    for (int h = 0; h < 2; ++h) {
+                        const float v0 = silu(acc[m][n + 2][2 * h]) * acc[m][n][2 * h];
+                        const float v1 = silu(acc[m][n + 2][2 * h + 1]) * acc[m][n][2 * h + 1];
+                        const uint16_t h0 = f2bf(v0), h1 = f2bf(v1);
+                        w[h] = (uint32_t)h0 | ((uint32_t)h1 << 16);
+                        wl[h] = (uint32_t)f2bf(v0 - bf2f(h0)) | ((uint32_t)f2bf(v1 - bf2f(h1)) << 16);
+                    }
+                    const size_t idx = (size_t)(row0 + row) * I + jb + wn * 32 + n * 16 + 4 * g;
+                    *reinterpret_cast<uint2*>(p.act + idx) = make_uint2(w[0], w[1]);
+                    if (p.act_lo) *reinterpret_cast<uint2*>(p.act_lo + idx) = make_uint2(wl[0], wl[1]);
                 }
-                const size_t idx = (size_t)(row0 + row) * I + jb + wn * 32 + n * 16 + 4 * g;
-                *reinterpret_cast<uint2*>(p.act + idx) = make_uint2(w[0], w[1]);
-                if (p.act_lo) *reinterpret_cast<uint2*>(p.act_lo + idx) = make_uint2(wl[0], wl[1]);
             }
         }
-    }
+    };
+    if (nrows - wm * 128 > 64)
+        compute(IntC<8>{});
+    else
+        compute(IntC<4>{});
 }
 
 hipError_t launch_gemm1_tile(const Plan& p, const uint8_t* hs, const float* hs_scale,
