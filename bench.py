@@ -20,11 +20,22 @@ HBM and MFMA rates this GPU achieves.
 Rank 0 prints ONE JSON line. ``roofline`` covers the dominant kernel
 (GEMM1+SwiGLU; at T=8192 bound by FP8 MFMA), with HBM traffic and the MFMA
 busy fraction from rocprofv3 counter passes; ``kernels`` gives both GEMMs'
-rooflines; ``call_roofline`` the whole call; ``sweep`` the other
-configurations, each with its dominant kernel's roofline and, at the
+rooflines; ``call_roofline`` the whole call; ``sweep`` every configuration
+(the headline included), each with its dominant kernel's roofline, a
+``parity`` block and, at the CPU reference configuration (T=16) and the
 metric's points (T = 1 with and without a local slot, 256, 8192), the CPU
 oracle timed on this host (``cpu_baseline``); ``quantize_fp8`` the
 activation quantiser that feeds the operator.
+
+``parity`` mirrors the per-workload correctness fields the reference
+harness prints beside its latency (scripts/run_local.py:65-78): after all
+GPU timing, the CPU oracle runs on the same seeded inputs (every token up to
+T = 1024, 256 tokens spread over [0, T) above) and the GPU output of the
+timed calls is compared with its fp32 accumulator: routing top-k set
+mismatches (must be 0) and tokens with a selection boundary within 4 fp32
+ulps, max absolute error, max relative error over the elements with
+|ref| >= 1 % of max|ref|, normwise error, and the fraction of elements
+outside |out - ref| <= 1e-2 |ref| + 1e-2 max|ref|.
 """
 from __future__ import annotations
 
@@ -58,11 +69,14 @@ GEMM1_FLOPS_PER_SLOT = 2 * 2 * I * H
 GEMM2_FLOPS_PER_SLOT = 2 * H * I
 
 HEADLINE = "c3_t8192"
-SWEEP = ["c1_t1", "c1_t1_local", "c1_t4", "c1_t16", "c1_t64", "t256", "c2_t1024_o0", "c3_t8192",
-         "c4_t14000_skew"]
-# The metric's points (T = 1 / 256 / 8192): each sweep entry of these carries
-# the CPU oracle timed on this host beside the GPU figures.
-METRIC_POINTS = ("c1_t1", "c1_t1_local", "t256", "c3_t8192")
+SWEEP = ["c0_t16", "c1_t1", "c1_t1_local", "c1_t4", "c1_t16", "c1_t64", "t256", "c2_t1024_o0",
+         "c3_t8192", "c4_t14000_skew"]
+# The CPU reference configuration (T = 16) and the metric's points (T = 1 /
+# 256 / 8192): each sweep entry of these carries the CPU oracle timed on this
+# host beside the GPU figures.
+CPU_POINTS = ("c0_t16", "c1_t1", "c1_t1_local", "t256", "c3_t8192")
+PARITY_ALL_T = 1024   # parity on every token up to this T, on a spread subset above
+PARITY_SUBSET = 256
 
 
 def log(msg):
@@ -230,8 +244,64 @@ def time_workload(wl, steps, warmup, trials=5, exact=True):
     # the dominant kernel: the GEMM launch that takes longest
     dom = max(res["kernels"], key=lambda k: res["phase_us"][k])
     res["roofline"] = dict(res["kernels"][dom], kernel=dom)
+    # the timed calls' output rows and routing for the parity check in the
+    # CPU leg (the call is deterministic: every call wrote the same bytes)
+    tok = parity_tokens(wl.T)
+    ids, _ = kernel.route(args[0], args[1], wl.routed_scaling_factor)
+    res["_check"] = {"tokens": tok, "out": out[tok.to(dev)].cpu(), "ids": ids[tok.to(dev)].cpu()}
     del args, out
     return res
+
+
+def parity_tokens(T):
+    """Every token up to PARITY_ALL_T, else PARITY_SUBSET spread over [0, T)
+    with the first and the last."""
+    if T <= PARITY_ALL_T:
+        return torch.arange(T)
+    return torch.unique(torch.linspace(0, T - 1, PARITY_SUBSET).round().long())
+
+
+def parity_block(wl, chk):
+    """The CPU oracle on the checked tokens of ``wl`` (tokens are independent,
+    so every per-token input is sliced) against the GPU rows of the timed
+    calls; see the module docstring for the fields."""
+    from oracle import ref_moe as R
+    tok = chk["tokens"]
+    t = wl.tensors
+    ng, kg, k = wl.routing
+    sub = [t["routing_logits"][tok], t["routing_bias"], t["hidden_states"][tok],
+           t["hidden_states_scale"][:, tok].contiguous(), t["gemm1_weights"],
+           t["gemm1_weights_scale"], t["gemm2_weights"], t["gemm2_weights_scale"],
+           wl.local_expert_offset, wl.routed_scaling_factor]
+    ref = R.moe_forward(*sub, n_group=ng, topk_group=kg, top_k=k)
+    rep = R.tolerance_report(chk["out"].float(), ref.acc)
+    o, r = chk["out"].double(), ref.acc.double()
+    big = r.abs() >= 0.01 * float(r.abs().max()) if r.numel() else r.bool()
+    max_rel = float(((o - r).abs()[big] / r.abs()[big]).max()) if big.any() else 0.0
+    mism = R.routing_set_mismatch(chk["ids"], ref.route.ids)
+    ties = R.near_tie_tokens(sub[0], sub[1], ng, kg, k)
+    return {"tokens_checked": int(tok.numel()), "of_tokens": wl.T,
+            "routing_set_mismatches": int(mism), "near_tie_tokens": int(ties),
+            "max_abs_err": float(f"{rep['max_abs_err']:.3e}"), "max_rel_err": float(f"{max_rel:.3e}"),
+            "normwise_rel": float(f"{rep['normwise_rel']:.3e}"),
+            "frac_outside": float(f"{rep['frac_bad']:.3e}"),
+            "pass": bool(mism == 0 and rep["n_bad"] == 0)}
+
+
+def compact(res):
+    """A sweep entry of the JSON line: the figures a reader compares across
+    configurations (the headline's full record stays at the top level)."""
+    keep = ("workload", "T", "slots", "active_experts", "us_per_call", "us_per_call_cold",
+            "us_per_call_graph", "gbps", "tflops", "roofline_frac", "mixed_roofline_frac")
+    out = {k: res[k] for k in keep}
+    out["phase_us"] = {k: round(v, 1) for k, v in res["phase_us"].items()}
+    rf = res["roofline"]
+    out["roofline"] = {k: rf[k] for k in ("kernel", "bound", "achieved", "unit", "frac", "avg_launch_us")
+                       if k in rf}
+    for k in ("parity", "cpu_baseline"):
+        if k in res:
+            out[k] = res[k]
+    return out
 
 
 def time_graph(args, out, steps, trials=5):
@@ -517,15 +587,13 @@ def cpu_baseline(wl, reps):
                       f"active experts, 1 warmup + {reps} timed, median"}
 
 
-def dequant_all_experts_us(wl):
-    """One pass of the CPU oracle's dequantisation over all 32 local experts'
-    weights, as a definition-style reference does on every call."""
+def full_dequant_call_us(wl):
+    """One whole call of the CPU oracle in the definition-style schedule that
+    dequantises all 32 local experts' weights on every call (one timed call
+    after the active-experts warmup)."""
     from oracle import ref_moe as R
-    t = wl.tensors
     t0 = time.perf_counter()
-    for e in range(t["gemm1_weights"].shape[0]):
-        R.dequant_blocks(t["gemm1_weights"][e], t["gemm1_weights_scale"][e])
-        R.dequant_blocks(t["gemm2_weights"][e], t["gemm2_weights_scale"][e])
+    R.moe_forward(*wl.args(), dequant_all_experts=True)
     return round((time.perf_counter() - t0) * 1e6, 1)
 
 
@@ -578,8 +646,11 @@ def main():
     wl = make(a.workload)
     log(f"[bench] inputs for {a.workload} ready in {time.time() - t_start:.1f}s")
     head = time_workload(wl, a.steps, a.warmup)
-    log(f"[bench] {json.dumps(head)}")
 
+    def loggable(r):
+        return {k: v for k, v in r.items() if not k.startswith("_")}
+
+    log(f"[bench] {json.dumps(loggable(head))}")
     sweep = []
     if a.sweep:
         for name in SWEEP:
@@ -589,9 +660,11 @@ def main():
             w = make(name)
             steps = a.steps if w.T <= 1024 else max(10, a.steps // 2)
             r = time_workload(w, steps, a.warmup, exact=False)
-            log(f"[bench] {json.dumps(r)}")
+            log(f"[bench] {json.dumps(loggable(r))}")
             sweep.append(r)
             del w
+    else:
+        sweep.append(head)
     quant = [time_quantizer(T) for T in (64, 8192)] if a.sweep else []
     for qr in quant:
         log(f"[bench] quantiser {qr}")
@@ -602,17 +675,24 @@ def main():
 
     cpu = None
     if not a.no_cpu:
-        # the CPU oracle at the headline and at every metric point of the sweep
-        # (1 timed call above T = 1024, 3 below), after all GPU timing
-        for r in ([head] + [r for r in sweep if r is not head and r["workload"] in METRIC_POINTS]):
+        # The CPU leg, after all GPU timing: the oracle checks every entry's
+        # GPU output (parity), and is timed at the CPU reference
+        # configuration and the metric's points (1 timed call above T = 1024,
+        # 3 below); at the headline also in the full-dequant schedule.
+        for r in sweep:
             w = make(r["workload"])
-            log(f"[bench] CPU oracle baseline {w.name} ...")
-            r["cpu_baseline"] = cpu_baseline(w, 1 if w.T > 1024 else 3)
-            log(f"[bench] cpu {w.name} {r['cpu_baseline']}")
-            if r is head:
-                r["cpu_baseline"]["dequant_all_experts_us"] = dequant_all_experts_us(w)
+            r["parity"] = parity_block(w, r.pop("_check"))
+            log(f"[bench] parity {w.name} {r['parity']}")
+            if r["workload"] in CPU_POINTS or r is head:
+                log(f"[bench] CPU oracle baseline {w.name} ...")
+                r["cpu_baseline"] = cpu_baseline(w, 1 if w.T > 1024 else 3)
+                if r is head:
+                    r["cpu_baseline"]["full_dequant_call_us"] = full_dequant_call_us(w)
+                log(f"[bench] cpu {w.name} {r['cpu_baseline']}")
             del w
         cpu = head["cpu_baseline"]
+    for r in sweep:
+        r.pop("_check", None)
 
     roof = dict(head["roofline"])
     if counters:
@@ -650,7 +730,8 @@ def main():
                           "phase_us": head["phase_us"]},
         "counters": counters,
         "cpu_baseline": cpu,
-        "sweep": sweep,
+        "parity": head.get("parity"),
+        "sweep": [compact(r) for r in sweep],
         "quantize_fp8": quant,
     }
     print(json.dumps(line), flush=True)

@@ -18,7 +18,7 @@ import sys
 import sysconfig
 from concurrent.futures import ThreadPoolExecutor
 
-from .shapes import DEFINITIONS, lib_name_of
+from .shapes import DEFINITIONS, definition_supported, lib_name_of
 
 HERE = os.path.dirname(os.path.abspath(__file__))
 CSRC = os.path.join(HERE, "csrc")
@@ -116,6 +116,9 @@ def build_host() -> str:
 
 
 def build(jobs: int = 8, extra=()) -> str:
+    bad = [d for d in DEFINITIONS if not definition_supported(d)]
+    if bad:
+        raise ValueError(f"unsupported definitions (see shapes.py): {bad}")
     os.makedirs(BUILD, exist_ok=True)
     jobs_list = [(s, d) for d in DEFINITIONS for s in SOURCES] + [(s, None) for s in PEAKS_SOURCES]
     with ThreadPoolExecutor(max_workers=jobs) as ex:

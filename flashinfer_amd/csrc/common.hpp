@@ -68,6 +68,10 @@ __device__ __forceinline__ emask_t ebit(int l) { return (emask_t)1 << l; }
 __device__ __forceinline__ int epopc(emask_t m) {
     if constexpr (EL > 32) return __popcll(m); else return __popc((uint32_t)m);
 }
+// The LDS-tiled GEMMs address weight rows of the shard with 32-bit signed
+// offsets ((e * N1 + row) * H for W1, (e * H + row) * I for W2).
+static_assert((long long)EL * N1 * H < (1LL << 31), "gemm1_weights of the shard exceed 2^31 bytes");
+static_assert((long long)EL * H * I < (1LL << 31), "gemm2_weights of the shard exceed 2^31 bytes");
 constexpr int BLK = 128;            // scale block
 constexpr int HB = H / BLK;         // k-blocks of GEMM1 (56 at H=7168)
 constexpr int IB = I / BLK;         // k-blocks of GEMM2 (16 at I=2048)

@@ -163,7 +163,9 @@ int run(py::handle logits_h, py::handle bias_h, py::handle hs_h, py::handle hss_
     if (!logits || !w1 || !out || logits->dim() != 2 || w1->dim() != 3 || !out->is_cuda())
         return NOT_FAST;
     const int64_t T = logits->size(0);
-    if (T == 0) return NOT_FAST;
+    // T = 0 and T past the library's limit take the general path, which
+    // returns or raises before any workspace is sized
+    if (T == 0 || T > MI_MOE_MAX_TOKENS) return NOT_FAST;
     const Def* d = find_def(w1->size(0), w1->size(1), w1->size(2), logits->size(1));
     if (!d) return NOT_FAST;
     const int64_t H = d->H, I = d->two_i / 2, EL = d->EL, EG = d->EG;

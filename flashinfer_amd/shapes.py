@@ -9,7 +9,10 @@ library. The 128-element scale blocks are fixed.
 
 Supported: H a multiple of 1024, I a multiple of 256, 16 / 32 / 64 local
 experts, 64 / 128 / 256 global experts in groups of 2 to 16 lanes' worth
-(group size / (global experts / 64) in {2, 4, 8, 16}), top_k <= 8.
+(group size / (global experts / 64) in {2, 4, 8, 16}), top_k <= 8, and a
+shard whose weights (local experts x 2I x H bytes of gemm1_weights) stay
+under 2^31 bytes: the LDS-tiled GEMMs address weight rows with 32-bit
+signed offsets.
 """
 from __future__ import annotations
 
@@ -75,7 +78,7 @@ def definition_supported(d: Definition) -> bool:
         return False
     lpg = (d.EG // d.NG) // (d.EG // 64)
     return (lpg in (2, 4, 8, 16) and 1 <= d.KG <= d.NG and 1 <= d.TOPK <= 8
-            and d.TOPK <= d.KG * (d.EG // d.NG))
+            and d.TOPK <= d.KG * (d.EG // d.NG) and d.EL * 2 * d.I * d.H < (1 << 31))
 
 
 def as_definition(x) -> Definition:

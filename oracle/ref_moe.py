@@ -179,17 +179,28 @@ def moe_forward(
     gemm1_weights, gemm1_weights_scale, gemm2_weights, gemm2_weights_scale,
     local_expert_offset, routed_scaling_factor,
     *, n_group=8, topk_group=4, top_k=8, acc_dtype=torch.float32, act_round=None,
+    dequant_all_experts=False,
 ) -> MoEResult:
     """The whole layer for one expert-parallel shard (kernel.py:600-825).
 
     Non-local experts contribute nothing; tokens with no local expert get a
     zero row (kernel.py:692-695, :801). Contributions are summed per token in
     ascending local-expert order, then cast to bf16 (kernel.py:822).
+
+    ``dequant_all_experts=True`` dequantises every local expert's weights
+    before routing, as a definition-style reference that materialises the
+    dequantised weight tensors does on every call; the result is the same,
+    only the work (and its CPU time) differs.
     """
     local_expert_offset = int(local_expert_offset)
     routed_scaling_factor = float(routed_scaling_factor)
     T, H = hidden_states.shape
     e_local = gemm1_weights.shape[0]
+    full = None
+    if dequant_all_experts:
+        full = [(dequant_blocks(gemm1_weights[e], gemm1_weights_scale[e], acc_dtype),
+                 dequant_blocks(gemm2_weights[e], gemm2_weights_scale[e], acc_dtype))
+                for e in range(e_local)]
     r = route(routing_logits, routing_bias, routed_scaling_factor, n_group, topk_group, top_k)
     slots = local_assignment(r.ids, r.weights, local_expert_offset, e_local)
     acc = torch.zeros(T, H, dtype=acc_dtype)
@@ -198,8 +209,14 @@ def moe_forward(
         for e, (tok, w) in enumerate(slots):
             if len(tok) == 0:
                 continue
-            o = expert_forward(a[tok], gemm1_weights[e], gemm1_weights_scale[e],
-                               gemm2_weights[e], gemm2_weights_scale[e], acc_dtype, act_round)
+            if full is None:
+                o = expert_forward(a[tok], gemm1_weights[e], gemm1_weights_scale[e],
+                                   gemm2_weights[e], gemm2_weights_scale[e], acc_dtype, act_round)
+            else:
+                x = swiglu(a[tok] @ full[e][0].t())
+                if act_round is not None:
+                    x = x.to(act_round).to(acc_dtype)
+                o = x @ full[e][1].t()
             acc.index_add_(0, tok, o * w.to(acc_dtype)[:, None])
     return MoEResult(output=acc.to(torch.bfloat16), route=r, acc=acc, slots=slots)
 

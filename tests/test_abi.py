@@ -264,6 +264,11 @@ def test_definition_registry_rejects_unsupported():
     assert not shapes.definition_supported(D(7168, 2048, TOPK=9))
     assert not shapes.definition_supported(D(7168, 2048, KG=9))
     assert shapes.definition_supported(D(7168, 2048, EG=64, NG=8, KG=2, TOPK=4, EL=16))
+    # the shard's gemm1_weights must stay under 2^31 bytes (32-bit signed
+    # weight-row offsets in the LDS-tiled GEMMs): 64 x 4096 x 7168 fits,
+    # 64 x 2 x 4096 x 8192 does not
+    assert shapes.definition_supported(D(7168, 2048, EL=64))
+    assert not shapes.definition_supported(D(8192, 4096, EL=64))
     with pytest.raises(ValueError, match="no library"):
         _lib.definition_for(7168, 2048, 16, 64)
 
@@ -329,3 +334,20 @@ def test_native_host_registration():
     kernel._HOST.register_definition(d.EL, 2 * d.I, d.H, d.EG, run_addr, size_addr)
     with pytest.raises(RuntimeError, match="another library"):
         kernel._HOST.register_definition(d.EL, 2 * d.I, d.H, d.EG, size_addr, size_addr)
+
+
+def test_oversize_t_raises_before_any_workspace(monkeypatch):
+    """T past MI_MOE_MAX_TOKENS is refused by the Python path before a
+    workspace is sized or allocated (the native host path hands such calls
+    to it): torch.empty tensors of the right shapes, never read."""
+    allocated = []
+    monkeypatch.setattr(kernel, "_workspace", lambda *a: allocated.append(a))
+    T = _lib.MI_MOE_MAX_TOKENS + 1
+    e = torch.empty
+    args = [e(T, 256), e(256, dtype=torch.bfloat16), e(T, 7168, dtype=torch.float8_e4m3fn),
+            e(56, T), e(32, 4096, 7168, dtype=torch.float8_e4m3fn), e(32, 32, 56),
+            e(32, 7168, 2048, dtype=torch.float8_e4m3fn), e(32, 56, 16), 0, 2.5,
+            e(T, 7168, dtype=torch.bfloat16)]
+    with pytest.raises(ValueError, match="MI_MOE_MAX_TOKENS"):
+        kernel.run(*args)
+    assert allocated == []

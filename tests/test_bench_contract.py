@@ -51,3 +51,59 @@ def test_counter_passes_never_start_under_a_profiler(monkeypatch):
     # an unrelated preload is not a profiler
     assert not bench.profiler_inherited({"LD_PRELOAD": "/usr/lib/libharness.so"})
     assert not bench.profiler_inherited({})
+
+
+def test_parity_block_pass_and_planted_error():
+    """The parity fields the bench prints per workload: the oracle's own bf16
+    output passes with zero routing mismatches; a planted error in one
+    element (made on the CPU) is counted outside the bar."""
+    import torch
+    from flashinfer_amd import workloads as W
+    wl = W.make_workload("tiny", T=40, seed=21, H=256, I=128, weight_seed=99)
+    tok = bench.parity_tokens(wl.T)
+    assert torch.equal(tok, torch.arange(40))
+    ref = R.moe_forward(*wl.args())
+    chk = {"tokens": tok, "out": ref.output.clone(), "ids": ref.route.ids.clone()}
+    p = bench.parity_block(wl, chk)
+    assert p["pass"] and p["routing_set_mismatches"] == 0 and p["frac_outside"] == 0.0
+    assert p["tokens_checked"] == 40 and p["of_tokens"] == 40
+    assert p["normwise_rel"] < 5e-3  # the bf16 rounding of the output alone
+    bad = dict(chk, out=chk["out"].clone())
+    r, c = divmod(int(ref.acc.abs().argmax()), 256)
+    bad["out"][r, c] = -bad["out"][r, c]
+    q = bench.parity_block(wl, bad)
+    assert not q["pass"] and q["frac_outside"] > 0 and q["max_rel_err"] >= 1.9
+    ids = chk["ids"].clone()
+    a0, a1 = int(ids[3, 0]), int(ids[3, 1])
+    ids[3, 0], ids[3, 1] = a1, a0  # order within a set does not count
+    assert bench.parity_block(wl, dict(chk, ids=ids))["routing_set_mismatches"] == 0
+    ids[5, 0] = (int(ids[5, 0]) + 1) % 256 if int(ids[5, 0]) + 1 not in ids[5].tolist() else 255
+    assert bench.parity_block(wl, dict(chk, ids=ids))["routing_set_mismatches"] == 1
+
+
+def test_parity_subset_spreads_over_large_t():
+    tok = bench.parity_tokens(14000)
+    assert tok[0] == 0 and tok[-1] == 13999 and len(tok) == bench.PARITY_SUBSET
+    assert torch_sorted(tok)
+
+
+def torch_sorted(t):
+    return bool((t[1:] > t[:-1]).all())
+
+
+def test_compact_sweep_entry_is_small():
+    import json
+    res = {"workload": "c3_t8192", "T": 8192, "slots": 11559, "active_experts": 28,
+           "us_per_call": 870.1, "us_per_call_cold": 900.2, "us_per_call_graph": 880.3,
+           "gbps": 1600.1, "tflops": 1150.2, "roofline_frac": 0.23, "mixed_roofline_frac": 0.31,
+           "phase_us": {"route": 12.34, "sort": 16.5, "gemm1_swiglu": 407.21, "gemm2": 380.4,
+                        "combine": 52.2},
+           "roofline": {"kernel": "gemm1_swiglu", "bound": "mfma", "achieved": 1666.9,
+                        "unit": "TFLOP/s", "frac": 0.3334, "avg_launch_us": 407.2, "mfma_dtype": "fp8",
+                        "algorithmic_bytes_per_launch": 1, "gbps": 2.0},
+           "kernels": {"gemm1_swiglu": {"x": 1}, "gemm2": {"y": 2}}, "trials_us": [1.0] * 5,
+           "parity": {"pass": True}, "cpu_baseline": {"value": 1.0}}
+    c = bench.compact(res)
+    assert "kernels" not in c and "trials_us" not in c and c["parity"] == {"pass": True}
+    assert set(c["roofline"]) == {"kernel", "bound", "achieved", "unit", "frac", "avg_launch_us"}
+    assert len(json.dumps(c)) < 900

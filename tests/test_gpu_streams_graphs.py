@@ -169,3 +169,48 @@ def test_graphs_at_increasing_sizes_keep_their_workspaces():
     for i in range(2):
         assert torch.equal(_bits(outs[i]), _bits(refs[i])), ("concurrent", i)
     del graphs
+
+
+def test_captured_workspaces_released_with_their_graphs():
+    """Each captured call allocates its workspace from the graph's private
+    pool and keeps no reference after the call: replays still equal eager
+    calls, and destroying the graphs returns device memory to where it was
+    before the captures."""
+    import gc
+    log("test_captured_workspaces_released_with_their_graphs")
+    wls = [W.standard("c1_t16"), W.standard("c1_t64"), W.standard("t256")]
+    statics = [gpu_args(wl) for wl in wls]
+    outs = [torch.empty(wl.T, H, dtype=torch.bfloat16, device="cuda") for wl in wls]
+    refs = [torch.empty_like(o) for o in outs]
+    for st, r in zip(statics, refs):
+        kernel.run(*st, r)
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        for st, o in zip(statics, outs):
+            kernel.run(*st, o)
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    gc.collect()
+    base = torch.cuda.memory_allocated()
+    graphs = []
+    for st, o in zip(statics, outs):
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g):
+            kernel.run(*st, o)
+        graphs.append(g)
+    torch.cuda.synchronize()
+    held = torch.cuda.memory_allocated() - base
+    for rep in range(3):
+        for i, g in enumerate(graphs):
+            outs[i].fill_(float("nan"))
+            g.replay()
+            torch.cuda.synchronize()
+            assert torch.equal(_bits(outs[i]), _bits(refs[i])), (rep, i)
+    del g, graphs
+    gc.collect()
+    torch.cuda.synchronize()
+    after = torch.cuda.memory_allocated()
+    log(f"  captured workspaces held {held / 2**20:.1f} MiB while the graphs lived; "
+        f"after their release {(after - base) / 2**20:.1f} MiB")
+    assert after <= base

@@ -236,6 +236,18 @@ def test_moe_linearity():
     assert torch.allclose(R.moe_forward(*args3, acc_dtype=torch.float64).acc, 2 * base, rtol=1e-12, atol=0)
 
 
+def test_moe_dequant_all_experts_schedule_same_result():
+    """The definition-style schedule (every expert's weights dequantised
+    before routing, as the bench's full-dequant CPU baseline runs it) gives
+    the same output; the per-token brute force above pins both."""
+    wl = _tiny_workload(T=24, seed=15, off=0)
+    a = R.moe_forward(*wl.args(), acc_dtype=torch.float64)
+    b = R.moe_forward(*wl.args(), acc_dtype=torch.float64, dequant_all_experts=True)
+    assert sum(len(tk) for tk, _ in a.slots) > 0
+    assert torch.allclose(a.acc, b.acc, rtol=1e-12, atol=1e-18)
+    assert torch.equal(a.output, b.output)
+
+
 def test_moe_empty_routing_is_zero():
     wl = _tiny_workload(T=8, seed=13, off=256)  # no expert is local
     res = R.moe_forward(*wl.args())

@@ -91,3 +91,49 @@ def test_noalloc_refuses_oversize_without_launch():
     assert b"MI_MOE_NOALLOC_MAX_TOKENS" in L.mi_moe_last_error()
     torch.cuda.synchronize()
     assert bool((out == 7.0).all())  # nothing was enqueued
+
+
+_CAPTURE_FIRST_CALL = r"""
+import ctypes, sys
+sys.path.insert(0, {root!r})
+sys.path.insert(0, {tests!r})
+import torch
+from _helpers import gpu_args
+from flashinfer_amd import _lib, kernel
+from flashinfer_amd import workloads as W
+wl = W.standard("c1_t64")
+args = gpu_args(wl)
+ref = torch.empty(wl.T, 7168, dtype=torch.bfloat16, device="cuda")
+kernel.run(*args, ref)  # loads the library and its kernels (mi_moe_run)
+out = torch.full_like(ref, float("nan"))
+torch.cuda.synchronize()
+g = torch.cuda.CUDAGraph()
+with torch.cuda.graph(g):
+    kernel.run_noalloc(*args, out)  # the first mi_moe_run_noalloc call of the process
+torch.cuda.synchronize()
+ok = []
+for rep in range(3):
+    out.fill_(float("nan"))
+    g.replay()
+    torch.cuda.synchronize()
+    ok.append(bool(torch.equal(out.view(torch.int16), ref.view(torch.int16))))
+    junk = torch.empty_like(ref)
+    kernel.run(*args, junk)  # eager work of the program between replays
+    torch.cuda.synchronize()
+print("REPLAYS", ok, flush=True)
+"""
+
+
+def test_noalloc_first_call_inside_graph_capture():
+    """In a fresh process, the first mi_moe_run_noalloc call (which looks up
+    the scratch's device address) is made inside a HIP graph capture; every
+    replay equals an eager mi_moe_run bit for bit."""
+    import os
+    import subprocess
+    import sys
+    log("test_noalloc_first_call_inside_graph_capture (child process)")
+    tests = os.path.dirname(os.path.abspath(__file__))
+    code = _CAPTURE_FIRST_CALL.format(root=os.path.dirname(tests), tests=tests)
+    r = subprocess.run([sys.executable, "-c", code], capture_output=True, text=True, timeout=300)
+    assert r.returncode == 0, r.stderr[-2000:]
+    assert "REPLAYS [True, True, True]" in r.stdout, (r.stdout, r.stderr[-2000:])
