@@ -47,11 +47,20 @@ static_assert((uint64_t)kMaxTokens * TOPK * I * 2 <= (1ull << 32), "GEMM2 tile r
 
 constexpr size_t align_up(size_t x) { return (x + 255) & ~(size_t)255; }
 
-// Largest T whose GEMM2 writes fp32 partial rows (and may run on the split
-// activation act + act_lo): the workspace reserves fp32 partials and act_lo
-// for these T. Up to here the call streams weights from HBM, and the wider
-// partials cost about 0.5% of the call.
-constexpr int64_t F32_PART_MAX_T = 256;
+// Largest T whose GEMM2 writes fp32 partial rows: the workspace reserves
+// 4-byte partials for these T. Measured per call on MI355X against bf16 rows
+// (same box, interleaved): under 1% up to T = 256, where weights stream from
+// HBM; +2.4% at T = 1024 (combine reads twice the bytes); +4.0% at T = 8192
+// and +7.9% at T = 14000 with every token on 8 experts, which keep bf16 rows.
+#ifndef MI_MOE_F32_PART_MAX_T
+#define MI_MOE_F32_PART_MAX_T 1024
+#endif
+constexpr int64_t F32_PART_MAX_T = MI_MOE_F32_PART_MAX_T;
+// Largest T for which the workspace reserves act_lo (the split activation
+// act + act_lo that MI_MOE_SPLIT_ACT=1 asks for; the LDS tiles have no split
+// path, so it stops where they take over).
+constexpr int64_t SPLIT_ACT_MAX_T = 256;
+static_assert(SPLIT_ACT_MAX_T <= F32_PART_MAX_T, "the split activation writes fp32 rows");
 
 constexpr mi_moe_layout make_layout(int64_t T) {
     mi_moe_layout L{};
@@ -65,9 +74,10 @@ constexpr mi_moe_layout make_layout(int64_t T) {
     L.sorted_w = o;   o = align_up(o + s_max * 4);
     L.tok_slot = o;   o = align_up(o + t * TOPK_LD * 4);
     L.chunk_cnt = o;  o = align_up(o + (size_t)sort_chunks((int)t) * EL * 4);
-    const bool split = (int64_t)t <= F32_PART_MAX_T;
+    const bool f32 = (int64_t)t <= F32_PART_MAX_T;
+    const bool split = (int64_t)t <= SPLIT_ACT_MAX_T;
     L.act = o;        o = align_up(o + s_max * I * 2);
-    L.part = o;       o = align_up(o + s_max * H * (split ? 4 : 2));
+    L.part = o;       o = align_up(o + s_max * H * (f32 ? 4 : 2));
     L.act_lo = o;     o = align_up(o + (split ? s_max * I * 2 : 0));
     L.total = o;
     return L;
@@ -208,13 +218,15 @@ int env_flag(const char* name) {  // -1 unset, else 0 / 1
 }
 
 // GEMM2's inputs and outputs (G2_*): fp32 partial rows up to F32_PART_MAX_T
-// tokens with every GEMM2 kernel but the LDS tiles (MI_MOE_F32_PARTIALS=0
-// turns them off); the split activation only when MI_MOE_SPLIT_ACT=1 asks
-// for it (measured on MI355X it adds 5-9% at T = 1, 4, 64 and 256, 1.6% at
-// T = 16: the second operand's loads and registers cost occupancy).
+// tokens (MI_MOE_F32_PARTIALS=0 turns them off); the split activation only
+// up to SPLIT_ACT_MAX_T, with a kernel other than the LDS tiles, and when
+// MI_MOE_SPLIT_ACT=1 asks for it (measured on MI355X it adds 5-9% at T = 1,
+// 4, 64 and 256, 1.6% at T = 16: the second operand's loads and registers
+// cost occupancy).
 int gemm2_mode_for(int64_t T, int g2) {
-    if (T > F32_PART_MAX_T || g2 == 3 || g2 == 4 || g2 == 18) return G2_BF16;
-    if (env_flag("MI_MOE_SPLIT_ACT") == 1) return G2_SPLIT;
+    if (T > F32_PART_MAX_T) return G2_BF16;
+    const bool tile = g2 == 3 || g2 == 4 || g2 == 18;
+    if (!tile && T <= SPLIT_ACT_MAX_T && env_flag("MI_MOE_SPLIT_ACT") == 1) return G2_SPLIT;
     return env_flag("MI_MOE_F32_PARTIALS") == 0 ? G2_BF16 : G2_F32;
 }
 

@@ -39,7 +39,7 @@ struct G2Tile {
     static_assert(2 * STAGE <= 160 * 1024, "LDS budget");
 };
 
-template <int WM, int WN, int GM>
+template <int WM, int WN, int GM, int MODE>
 __global__ __launch_bounds__(64 * WM * WN) void gemm2_tile_kernel(Plan p,
                                                                   const uint8_t* __restrict__ w2,
                                                                   const float* __restrict__ w2s) {
@@ -169,7 +169,8 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm2_tile_kernel(Plan p,
         __syncthreads();
     }
 
-    // Epilogue: routing weight (kernel.py:364) and bf16 store for the combine.
+    // Epilogue: routing weight (kernel.py:364) and a bf16 (MODE G2_BF16) or
+    // fp32 (G2_F32) row for the combine.
 #pragma unroll
     for (int m = 0; m < 4; ++m) {
 #pragma unroll
@@ -177,9 +178,14 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm2_tile_kernel(Plan p,
             const int row = wm * 64 + m * 16 + g * 4 + i;
             if (row < nrows) {
                 const float w = w_lds[row];
-                uint16_t* dst = p.part + (size_t)(row0 + row) * H + n0 + wn * 64 + r;
+                const size_t o = (size_t)(row0 + row) * H + n0 + wn * 64 + r;
 #pragma unroll
-                for (int n = 0; n < 4; ++n) dst[n * 16] = f2bf(w * acc[m][n][i]);
+                for (int n = 0; n < 4; ++n) {
+                    if constexpr (MODE == G2_F32)
+                        p.part_f32[o + n * 16] = w * acc[m][n][i];
+                    else
+                        p.part[o + n * 16] = f2bf(w * acc[m][n][i]);
+                }
             }
         }
     }
@@ -187,16 +193,23 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm2_tile_kernel(Plan p,
 
 hipError_t launch_gemm2_tile(const Plan& p, const uint8_t* w2, const float* w2s, int variant,
                              hipStream_t s) {
+    const bool f32 = gemm2_mode(p) != G2_BF16;
     if (variant == 3 || variant == 18) {
         using C = G2Tile<2, 4>;
         const int tiles = max_mtiles(p.T, C::BM) * C::NT;
         dim3 grid((tiles + 7) / 8 * 8);
-        hipLaunchKernelGGL((gemm2_tile_kernel<2, 4, 4>), grid, dim3(C::THREADS), 0, s, p, w2, w2s);
+        if (f32)
+            hipLaunchKernelGGL((gemm2_tile_kernel<2, 4, 4, G2_F32>), grid, dim3(C::THREADS), 0, s, p, w2, w2s);
+        else
+            hipLaunchKernelGGL((gemm2_tile_kernel<2, 4, 4, G2_BF16>), grid, dim3(C::THREADS), 0, s, p, w2, w2s);
     } else {
         using C = G2Tile<1, 4>;
         const int tiles = max_mtiles(p.T, C::BM) * C::NT;
         dim3 grid((tiles + 7) / 8 * 8);
-        hipLaunchKernelGGL((gemm2_tile_kernel<1, 4, 4>), grid, dim3(C::THREADS), 0, s, p, w2, w2s);
+        if (f32)
+            hipLaunchKernelGGL((gemm2_tile_kernel<1, 4, 4, G2_F32>), grid, dim3(C::THREADS), 0, s, p, w2, w2s);
+        else
+            hipLaunchKernelGGL((gemm2_tile_kernel<1, 4, 4, G2_BF16>), grid, dim3(C::THREADS), 0, s, p, w2, w2s);
     }
     return hipGetLastError();
 }

@@ -81,7 +81,7 @@ typedef struct mi_moe_args {
  *   chunk_cnt  int32 [ceil(T/1024), E]  per-1024-token-chunk local expert counts
  *   act        bf16  [kT, 2048]  SwiGLU(GEMM1) per slot, rounded to bf16
  *   part       bf16  [kT, 7168]  routing weight x GEMM2 row per slot; fp32
- *                             (same offset, twice the bytes) at T <= 256
+ *                             (same offset, twice the bytes) at T <= 1024
  *   act_lo     bf16  [kT, 2048]  SwiGLU(GEMM1) - act, reserved at T <= 256
  *                             (empty above) and written when the environment
  *                             sets MI_MOE_SPLIT_ACT=1: GEMM2 then multiplies

@@ -71,6 +71,19 @@ def test_workspace_layout_monotone_and_aligned():
         prev = L.total
 
 
+def test_workspace_reserves_fp32_rows_to_1024_and_act_lo_to_256():
+    """fp32 partial rows (4 bytes per element) up to T = 1024, bf16 above;
+    act_lo (the split activation) only up to T = 256."""
+    def sizes(T):
+        L = _lib.workspace_layout(T)
+        return L.act_lo - L.part, L.total - L.act_lo
+    slots = lambda T: 8 * T  # noqa: E731
+    for T, part_bytes, lo_bytes in ((256, 4, 2), (257, 4, 0), (1024, 4, 0), (1025, 2, 0)):
+        part, lo = sizes(T)
+        assert slots(T) * 7168 * part_bytes <= part < slots(T) * 7168 * part_bytes + 256, T
+        assert slots(T) * 2048 * lo_bytes <= lo < slots(T) * 2048 * lo_bytes + 256, T
+
+
 def _args(**over):
     a = _lib.MiMoeArgs()
     ptr = 1 << 20  # 256-byte aligned fake addresses: never dereferenced on these paths
