@@ -25,16 +25,23 @@
 // read at the same k offsets (ld_afrag).
 //
 // With FRONT_SORT (T <= 64, MT = 1) the kernel also stands in for the sort
-// launch: each wave derives its row tile and its rows' tokens from the top-k
-// ids (wave_tile: the one-wave sort's counts and scan, in registers), so no
-// kernel boundary separates routing from GEMM1, and workgroup (0, 0) writes
-// the sort's tables (expert offsets, tile prefixes for bm1 / bm2, slot lists)
-// for GEMM2 and the combine, which run after this kernel. With FRONT_ROUTE
-// every workgroup first routes all T tokens itself (its waves take them
-// round-robin, route_token as in the routing kernel) into LDS, and
-// workgroup (0, 0) also writes the top-k: the call then starts with GEMM1.
+// launch: each wave builds the row-tile table from the top-k ids in its
+// registers (wave_table: the one-wave sort's counts and scans) and looks up
+// its row tiles there, so no kernel boundary separates routing from GEMM1.
+// Workgroup 0 of the (one-dimensional) grid writes the sort's tables
+// (expert offsets, tile prefixes for bm1 / bm2, slot lists) for GEMM2 and
+// the combine, which run after this kernel, so no GEMM workgroup waits on
+// them. With FRONT_ROUTE every workgroup first
+// routes all T tokens itself (its waves take them round-robin, route_token
+// as in the routing kernel) into LDS, and the tables workgroup also writes
+// the top-k: the call then starts with GEMM1. A front workgroup takes row
+// tiles y, y + R, y + 2R, ... (R rows of workgroups): at T <= 4 the grid has
+// fewer rows than the bound on row tiles, most of which are empty there,
+// and every workgroup pays for the routing.
 #include "route_impl.hpp"
 #include "sort_impl.hpp"
+
+#include <algorithm>
 
 namespace mimoe {
 
@@ -56,15 +63,148 @@ void gemm1_stream_kernel(Plan p, const uint8_t* __restrict__ hs, const float* __
     __shared__ __attribute__((aligned(16))) int s_ids[RT];
     __shared__ __attribute__((aligned(16))) float s_w[RT];
 
-    const int tid = threadIdx.x;
-    const int lane = tid & 63;
-    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const int r = lane & 15, g = lane >> 4;
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
 
-    // Row tile and the tokens of this lane's rows (row i * 16 + r).
-    int e, row0, nrows;
-    int tok[MT];
+    // The GEMM of one row tile (expert e, slots row0 .. row0 + nrows - 1, the
+    // token of this lane's row i * 16 + r in tok[i]) for this workgroup's
+    // weight columns. The lane index comes in as an argument: the tile loop
+    // of the front kernels passes it through an empty asm statement, so the
+    // compiler recomputes the lane's addresses per tile instead of holding
+    // them across the loop (77 instead of 96 VGPRs and spills).
+    auto tile = [&](int e, const int row0, const int nrows, const int (&tok)[MT], const int lane,
+                    const int col) __attribute__((always_inline)) {
+        const int r = lane & 15, g = lane >> 4;
+        const int tid = wave * 64 + lane;
+        const int wc = wave % NW;         // column group
+        const int ks = wave / NW;         // k split: k-blocks [ks*KB, ks*KB + KB)
+        const int j0 = col * (16 * NW) + wc * 16;
+        // weights of expert e through a buffer resource: gate rows, then up rows I further
+        e = __builtin_amdgcn_readfirstlane(e);
+        const __amdgpu_buffer_rsrc_t wr = wrsrc(w1 + (size_t)e * N1 * H, (uint32_t)((size_t)N1 * H));
+        const uint32_t bg_off = (uint32_t)((size_t)j0 * H + (size_t)ks * KB * BLK + wl_off(lane, H));
+        const uint32_t bu_off = bg_off + (uint32_t)((size_t)I * H);
+        const uint8_t* a_ptr[MT];
+#pragma unroll
+        for (int i = 0; i < MT; ++i) a_ptr[i] = hs + (size_t)tok[i] * H + ks * KB * BLK + g * 32;
+        const float* sbg_ptr = w1s + ((size_t)e * N1B + j0 / BLK) * HB + ks * KB;
+        const float* sbu_ptr = w1s + ((size_t)e * N1B + (I + j0) / BLK) * HB + ks * KB;
+        const float (*sa_k)[BM] = sa_lds + ks * KB;  // this wave's k-blocks
+
+        WRaw bg[D], bu[D];
+        v8i a[D][MT];
+        v4f accg[MT], accu[MT];
+        const v4f zero = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int i = 0; i < MT; ++i) { accg[i] = zero; accu[i] = zero; }
+
+        // Consume ring stage d (k-block kb): two MFMAs per row sub-tile, block
+        // scales applied in fp32.
+        auto compute = [&](int d, int kb) __attribute__((always_inline)) {
+            const float sg = sbg_ptr[kb];
+            const float su = sbu_ptr[kb];
+            const v8i fg = wl_frag(bg[d]);
+            const v8i fu = wl_frag(bu[d]);
+#pragma unroll
+            for (int i = 0; i < MT; ++i) {
+                const v4f pg = mfma_f8_16x16x128(a[d][i], fg, zero);
+                const v4f pu = mfma_f8_16x16x128(a[d][i], fu, zero);
+                const float4 sa4 = *reinterpret_cast<const float4*>(&sa_k[kb][i * 16 + g * 4]);
+                accg[i][0] += pg[0] * (sa4.x * sg);
+                accg[i][1] += pg[1] * (sa4.y * sg);
+                accg[i][2] += pg[2] * (sa4.z * sg);
+                accg[i][3] += pg[3] * (sa4.w * sg);
+                accu[i][0] += pu[0] * (sa4.x * su);
+                accu[i][1] += pu[1] * (sa4.y * su);
+                accu[i][2] += pu[2] * (sa4.z * su);
+                accu[i][3] += pu[3] * (sa4.w * su);
+            }
+        };
+        auto load = [&](int d, int kb) __attribute__((always_inline)) {
+            const int nk = kb * BLK;
+            bg[d] = ld_wraw<NT>(wr, bg_off + nk, 8 * H);
+            bu[d] = ld_wraw<NT>(wr, bu_off + nk, 8 * H);
+#pragma unroll
+            for (int i = 0; i < MT; ++i) a[d][i] = ld_afrag(a_ptr[i] + nk);
+        };
+
+        // Start streaming weights first; the activation scales of the tile go to
+        // LDS while those loads are in flight.
+#pragma unroll
+        for (int d = 0; d < D; ++d) load(d, d);
+        // (64 * NW * KS is a multiple of BM, so entry i's row m = i % BM is the
+        // same for all of a thread's entries: row tid % BM = i' * 16 + r.)
+        static_assert((64 * NW * KS) % BM == 0, "scale loader row");
+        {
+            const int tok_m = tok[(tid % BM) / 16];
+            for (int i = tid; i < HB * BM; i += 64 * NW * KS) {
+                const int kb = i / BM, m = i % BM;
+                sa_lds[kb][m] = hs_scale[(size_t)kb * p.T + tok_m];
+            }
+        }
+        __syncthreads();
+
+        // Steady state: every stage is refilled right after it is consumed.
+#pragma unroll 1
+        for (int kb0 = 0; kb0 < KB - D; kb0 += D) {
+#pragma unroll
+            for (int d = 0; d < D; ++d) {
+                compute(d, kb0 + d);
+                load(d, kb0 + d + D);
+            }
+        }
+        // Drain the last D k-blocks.
+#pragma unroll
+        for (int d = 0; d < D; ++d) compute(d, KB - D + d);
+
+        // K split: the other waves of the column group hand their partial sums to
+        // the first through LDS, which adds them in split order (deterministic).
+        if constexpr (KS > 1) {
+            if (ks > 0) {
+#pragma unroll
+                for (int i = 0; i < MT; ++i)
+#pragma unroll
+                    for (int rr = 0; rr < 4; ++rr) {
+                        red[ks - 1][wc][8 * i + rr][lane] = accg[i][rr];
+                        red[ks - 1][wc][8 * i + 4 + rr][lane] = accu[i][rr];
+                    }
+            }
+            __syncthreads();
+            if (ks > 0) return;
+#pragma unroll
+            for (int k = 0; k < KS - 1; ++k)
+#pragma unroll
+                for (int i = 0; i < MT; ++i)
+#pragma unroll
+                    for (int rr = 0; rr < 4; ++rr) {
+                        accg[i][rr] += red[k][wc][8 * i + rr][lane];
+                        accu[i][rr] += red[k][wc][8 * i + 4 + rr][lane];
+                    }
+        }
+
+#pragma unroll
+        for (int i = 0; i < MT; ++i) {
+#pragma unroll
+            for (int rr = 0; rr < 4; ++rr) {
+                const int m = i * 16 + g * 4 + rr;
+                if (m < nrows) {
+                    const float v = silu(accu[i][rr]) * accg[i][rr];
+                    store_act(p, (size_t)(row0 + m) * I + j0 + r, v);
+                }
+            }
+        }
+    };
+
     if constexpr (FRONT != FRONT_NONE) {
+        // One-dimensional grid: workgroup 0 writes the tables (dispatched
+        // first, so it runs beside the GEMM workgroups, not after them);
+        // workgroup 1 + row * NCOL + col takes column block col of row tiles
+        // row, row + rows, ...
+        constexpr int NCOL = I / (16 * NW);
+        const int rows = (gridDim.x - 1) / NCOL;
+        const bool tables = blockIdx.x == 0;
+        const int col = tables ? 0 : (int)(blockIdx.x - 1) % NCOL;
+        const int row = tables ? 0 : (int)(blockIdx.x - 1) / NCOL;
         const int* ids_src = p.topk_ids;
         const float* w_src = p.topk_w;
         if constexpr (FRONT == FRONT_ROUTE) {
@@ -78,147 +218,39 @@ void gemm1_stream_kernel(Plan p, const uint8_t* __restrict__ hs, const float* __
             ids_src = s_ids;
             w_src = s_w;
         }
-        const WaveTile wt = wave_tile(p, ids_src, lane, blockIdx.y, BM);
-        if (blockIdx.x == 0 && blockIdx.y == 0 && wave == 0) {
-            if constexpr (FRONT == FRONT_ROUTE) {
-                if (lane < p.T) {  // the global top-k, as the routing kernel writes it
-                    int4* io = reinterpret_cast<int4*>(p.topk_ids + (size_t)lane * TOPK_LD);
-                    float4* wo = reinterpret_cast<float4*>(p.topk_w + (size_t)lane * TOPK_LD);
-                    io[0] = reinterpret_cast<const int4*>(s_ids + lane * TOPK_LD)[0];
-                    io[1] = reinterpret_cast<const int4*>(s_ids + lane * TOPK_LD)[1];
-                    wo[0] = reinterpret_cast<const float4*>(s_w + lane * TOPK_LD)[0];
-                    wo[1] = reinterpret_cast<const float4*>(s_w + lane * TOPK_LD)[1];
+        if (tables) {
+            if (wave == 0) {
+                if constexpr (FRONT == FRONT_ROUTE) {
+                    if (lane < p.T) {  // the global top-k, as the routing kernel writes it
+                        int4* io = reinterpret_cast<int4*>(p.topk_ids + (size_t)lane * TOPK_LD);
+                        float4* wo = reinterpret_cast<float4*>(p.topk_w + (size_t)lane * TOPK_LD);
+                        io[0] = reinterpret_cast<const int4*>(s_ids + lane * TOPK_LD)[0];
+                        io[1] = reinterpret_cast<const int4*>(s_ids + lane * TOPK_LD)[1];
+                        wo[0] = reinterpret_cast<const float4*>(s_w + lane * TOPK_LD)[0];
+                        wo[1] = reinterpret_cast<const float4*>(s_w + lane * TOPK_LD)[1];
+                    }
                 }
+                sort_one_wave<1>(p, ids_src, w_src, fa.bm1, fa.bm2, lane);
             }
-            sort_one_wave<1>(p, ids_src, w_src, fa.bm1, fa.bm2, lane);
+            return;
         }
-        if (!wt.valid) return;  // the same for every wave of the workgroup
-        e = wt.e;
-        row0 = wt.row0;
-        nrows = wt.nrows;
-        tok[0] = nth_set_bit(wt.hits, wt.rank0 + min(r, nrows - 1));
+        const WaveTable tab = wave_table(p, ids_src, lane, BM);
+        const int ntiles = table_tiles(tab);
+        for (int mt = row; mt < ntiles; mt += rows) {
+            const WaveTile wt = table_tile(tab, lane, mt, BM);
+            const int tok[MT] = {nth_set_bit(wt.hits, wt.rank0 + min(lane & 15, wt.nrows - 1))};
+            if (mt != row) __syncthreads();  // the last tile's reads of sa_lds are done
+            int ln = lane;
+            asm volatile("" : "+v"(ln));
+            tile(wt.e, wt.row0, wt.nrows, tok, ln, col);
+        }
     } else {
+        int e, row0, nrows;
         if (!find_tile(p.meta, META_MTILE1, blockIdx.y, BM, e, row0, nrows)) return;
+        int tok[MT];
 #pragma unroll
-        for (int i = 0; i < MT; ++i) tok[i] = p.sorted_tok[row0 + min(i * 16 + r, nrows - 1)];
-    }
-
-    const int wc = wave % NW;         // column group
-    const int ks = wave / NW;         // k split: k-blocks [ks*KB, ks*KB + KB)
-    const int j0 = blockIdx.x * (16 * NW) + wc * 16;
-    // weights of expert e through a buffer resource: gate rows, then up rows I further
-    e = __builtin_amdgcn_readfirstlane(e);
-    const __amdgpu_buffer_rsrc_t wr = wrsrc(w1 + (size_t)e * N1 * H, (uint32_t)((size_t)N1 * H));
-    const uint32_t bg_off = (uint32_t)((size_t)j0 * H + (size_t)ks * KB * BLK + wl_off(lane, H));
-    const uint32_t bu_off = bg_off + (uint32_t)((size_t)I * H);
-    const uint8_t* a_ptr[MT];
-#pragma unroll
-    for (int i = 0; i < MT; ++i) a_ptr[i] = hs + (size_t)tok[i] * H + ks * KB * BLK + g * 32;
-    const float* sbg_ptr = w1s + ((size_t)e * N1B + j0 / BLK) * HB + ks * KB;
-    const float* sbu_ptr = w1s + ((size_t)e * N1B + (I + j0) / BLK) * HB + ks * KB;
-    const float (*sa_k)[BM] = sa_lds + ks * KB;  // this wave's k-blocks
-
-    WRaw bg[D], bu[D];
-    v8i a[D][MT];
-    v4f accg[MT], accu[MT];
-    const v4f zero = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-    for (int i = 0; i < MT; ++i) { accg[i] = zero; accu[i] = zero; }
-
-    // Consume ring stage d (k-block kb): two MFMAs per row sub-tile, block
-    // scales applied in fp32.
-    auto compute = [&](int d, int kb) __attribute__((always_inline)) {
-        const float sg = sbg_ptr[kb];
-        const float su = sbu_ptr[kb];
-        const v8i fg = wl_frag(bg[d]);
-        const v8i fu = wl_frag(bu[d]);
-#pragma unroll
-        for (int i = 0; i < MT; ++i) {
-            const v4f pg = mfma_f8_16x16x128(a[d][i], fg, zero);
-            const v4f pu = mfma_f8_16x16x128(a[d][i], fu, zero);
-            const float4 sa4 = *reinterpret_cast<const float4*>(&sa_k[kb][i * 16 + g * 4]);
-            accg[i][0] += pg[0] * (sa4.x * sg);
-            accg[i][1] += pg[1] * (sa4.y * sg);
-            accg[i][2] += pg[2] * (sa4.z * sg);
-            accg[i][3] += pg[3] * (sa4.w * sg);
-            accu[i][0] += pu[0] * (sa4.x * su);
-            accu[i][1] += pu[1] * (sa4.y * su);
-            accu[i][2] += pu[2] * (sa4.z * su);
-            accu[i][3] += pu[3] * (sa4.w * su);
-        }
-    };
-    auto load = [&](int d, int kb) __attribute__((always_inline)) {
-        const int nk = kb * BLK;
-        bg[d] = ld_wraw<NT>(wr, bg_off + nk, 8 * H);
-        bu[d] = ld_wraw<NT>(wr, bu_off + nk, 8 * H);
-#pragma unroll
-        for (int i = 0; i < MT; ++i) a[d][i] = ld_afrag(a_ptr[i] + nk);
-    };
-
-    // Start streaming weights first; the activation scales of the tile go to
-    // LDS while those loads are in flight.
-#pragma unroll
-    for (int d = 0; d < D; ++d) load(d, d);
-    // (64 * NW * KS is a multiple of BM, so entry i's row m = i % BM is the
-    // same for all of a thread's entries: row tid % BM = i' * 16 + r.)
-    static_assert((64 * NW * KS) % BM == 0, "scale loader row");
-    {
-        const int tok_m = tok[(tid % BM) / 16];
-        for (int i = tid; i < HB * BM; i += 64 * NW * KS) {
-            const int kb = i / BM, m = i % BM;
-            sa_lds[kb][m] = hs_scale[(size_t)kb * p.T + tok_m];
-        }
-    }
-    __syncthreads();
-
-    // Steady state: every stage is refilled right after it is consumed.
-#pragma unroll 1
-    for (int kb0 = 0; kb0 < KB - D; kb0 += D) {
-#pragma unroll
-        for (int d = 0; d < D; ++d) {
-            compute(d, kb0 + d);
-            load(d, kb0 + d + D);
-        }
-    }
-    // Drain the last D k-blocks.
-#pragma unroll
-    for (int d = 0; d < D; ++d) compute(d, KB - D + d);
-
-    // K split: the other waves of the column group hand their partial sums to
-    // the first through LDS, which adds them in split order (deterministic).
-    if constexpr (KS > 1) {
-        if (ks > 0) {
-#pragma unroll
-            for (int i = 0; i < MT; ++i)
-#pragma unroll
-                for (int rr = 0; rr < 4; ++rr) {
-                    red[ks - 1][wc][8 * i + rr][lane] = accg[i][rr];
-                    red[ks - 1][wc][8 * i + 4 + rr][lane] = accu[i][rr];
-                }
-        }
-        __syncthreads();
-        if (ks > 0) return;
-#pragma unroll
-        for (int k = 0; k < KS - 1; ++k)
-#pragma unroll
-            for (int i = 0; i < MT; ++i)
-#pragma unroll
-                for (int rr = 0; rr < 4; ++rr) {
-                    accg[i][rr] += red[k][wc][8 * i + rr][lane];
-                    accu[i][rr] += red[k][wc][8 * i + 4 + rr][lane];
-                }
-    }
-
-#pragma unroll
-    for (int i = 0; i < MT; ++i) {
-#pragma unroll
-        for (int rr = 0; rr < 4; ++rr) {
-            const int m = i * 16 + g * 4 + rr;
-            if (m < nrows) {
-                const float v = silu(accu[i][rr]) * accg[i][rr];
-                store_act(p, (size_t)(row0 + m) * I + j0 + r, v);
-            }
-        }
+        for (int i = 0; i < MT; ++i) tok[i] = p.sorted_tok[row0 + min(i * 16 + (lane & 15), nrows - 1)];
+        tile(e, row0, nrows, tok, lane, blockIdx.x);
     }
 }
 
@@ -238,11 +270,23 @@ int gemm1_bm(int variant) {
     }
 }
 
+// Workgroup rows of the front kernels: at T <= 4 one per possible local
+// expert of a single token (a row takes tiles y, y + 8, ...), so a call
+// with a few active experts runs ~8 x 128 workgroups instead of the bound on
+// row tiles (up to 32 x 128), each of which would route the tokens first.
+constexpr int FRONT_ROWS_SMALL_T = 4;
+constexpr int FRONT_ROWS = TOPK;
+
 template <int MT, int D, int NW, int KS = 1, int FRONT = FRONT_NONE>
 static void launch_stream1(const Plan& p, const uint8_t* hs, const float* hs_scale,
                            const uint8_t* w1, const float* w1s, hipStream_t s,
                            const FrontArgs& fa = FrontArgs{}) {
     dim3 grid(I / (16 * NW), max_mtiles(p.T, 16 * MT));
+    if constexpr (FRONT != FRONT_NONE) {
+        // one-dimensional: the tables workgroup, then rows x column blocks
+        const int rows = p.T <= FRONT_ROWS_SMALL_T ? std::min<int>(grid.y, FRONT_ROWS) : (int)grid.y;
+        grid = dim3(1 + grid.x * rows, 1);
+    }
     if (wt_nt(p.T, 16 * MT))
         hipLaunchKernelGGL((gemm1_stream_kernel<MT, D, NW, KS, FRONT, true>), grid, dim3(64 * NW * KS), 0,
                            s, p, hs, hs_scale, w1, w1s, fa);

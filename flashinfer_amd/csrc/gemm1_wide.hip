@@ -89,7 +89,7 @@ __global__ __launch_bounds__(64 * WIDE_NW) void gemm1_wide_kernel(Plan p, const 
             if (lane == x) s_bal[wave][x] = bal;
         }
         __syncthreads();
-        // lane x < 32: expert x's count over the chunks; prefixes as in wave_tile
+        // lane x < 32: expert x's count over the chunks; prefixes as in wave_table
         unsigned long long b[WIDE_NW];
         int cnt = 0;
 #pragma unroll

@@ -195,55 +195,68 @@ __device__ __forceinline__ int nth_set_bit(unsigned long long mask, int k) {
     return pos;
 }
 
-// Row tile `mt` of bm-row tiles in the slot order of sort_one_wave, found by
-// the calling wave from the top-k ids alone (ids_base: [T, TOPK_LD], global or
-// LDS; T <= 64; every lane calls):
-// expert e, first slot row0 = expert_off[e] + rank0, rows, and the mask of
-// tokens (bit t = token t) that picked e. valid is false past the last tile.
-struct WaveTile {
-    int e, row0, nrows, rank0;
-    unsigned long long hits;
-    bool valid;
+// Row tiles of bm rows in the slot order of sort_one_wave, for kernels that
+// find their row tiles from the top-k ids alone (T <= 64): every wave builds
+// the table in its registers (wave_table: the one-wave sort's counts and
+// scans; lane t holds token t's local-expert mask, lane e < EL expert e's
+// slot count, exclusive slot prefix and inclusive row-tile prefix) and reads
+// a tile's entry with readlanes (table_tile).
+struct WaveTable {
+    emask_t m;     // lane t: local experts of token t
+    int cnt, s0;   // lane e: slots of expert e, exclusive prefix (expert_off[e])
+    int v1;        // lane e: inclusive prefix of the row tiles
 };
 
-__device__ __forceinline__ WaveTile wave_tile(const Plan& p, const int* ids_base, int lane, int mt,
-                                              int bm) {
-    emask_t m = 0;
+// ids_base: [T, TOPK_LD], global or LDS. Every lane of the wave calls.
+__device__ __forceinline__ WaveTable wave_table(const Plan& p, const int* ids_base, int lane, int bm) {
+    WaveTable w;
+    w.m = 0;
     if (lane < p.T) {
         int ids[TOPK];
         load_topk_ids(ids_base + (size_t)lane * TOPK_LD, ids);
 #pragma unroll
         for (int k = 0; k < TOPK; ++k) {
             const int l = ids[k] - p.local_offset;
-            m |= (unsigned)l < (unsigned)EL ? ebit(l) : (emask_t)0;
+            w.m |= (unsigned)l < (unsigned)EL ? ebit(l) : (emask_t)0;
         }
     }
     int cnt = 0;
 #pragma unroll
     for (int e = 0; e < EL; ++e) {
-        const unsigned long long bal = __ballot((m >> e) & 1);
+        const unsigned long long bal = __ballot((w.m >> e) & 1);
         if (lane == e) cnt = __popcll(bal);
     }
-    // inclusive prefixes of slots and row tiles over lanes 0..EL-1 (lane = expert)
     const int tiles = (cnt + bm - 1) / bm;
-    const int v0 = excl_prefix_small(cnt) + cnt;
-    const int v1 = excl_prefix_small(tiles) + tiles;
-    WaveTile w;
-    w.valid = mt < __builtin_amdgcn_readlane(v1, EL - 1);
-    w.e = w.row0 = w.nrows = w.rank0 = 0;
-    w.hits = 0;
-    if (!w.valid) return w;
-    // experts wholly before tile mt
-    const int ee = __popcll(__ballot(lane < EL && v1 <= mt));
-    const int t0 = __builtin_amdgcn_readlane(v1 - tiles, ee);
-    const int s0 = __builtin_amdgcn_readlane(v0 - cnt, ee);
-    const int ce = __builtin_amdgcn_readlane(cnt, ee);
-    w.e = ee;
-    w.rank0 = (mt - t0) * bm;
-    w.row0 = s0 + w.rank0;
-    w.nrows = min(bm, ce - w.rank0);
-    w.hits = __ballot((m >> ee) & 1);
+    w.cnt = cnt;
+    w.s0 = excl_prefix_small(cnt);
+    w.v1 = excl_prefix_small(tiles) + tiles;
     return w;
+}
+
+__device__ __forceinline__ int table_tiles(const WaveTable& w) {
+    return __builtin_amdgcn_readlane(w.v1, EL - 1);
+}
+
+// Row tile mt (0 <= mt < table_tiles) of the table: expert e, first slot
+// row0 = expert_off[e] + rank0, rows, and the mask of tokens (bit t = token
+// t) that picked e.
+struct WaveTile {
+    int e, row0, nrows, rank0;
+    unsigned long long hits;
+};
+
+__device__ __forceinline__ WaveTile table_tile(const WaveTable& w, int lane, int mt, int bm) {
+    // experts wholly before tile mt
+    const int ee = __popcll(__ballot(lane < EL && w.v1 <= mt));
+    const int ce = __builtin_amdgcn_readlane(w.cnt, ee);
+    const int t0 = __builtin_amdgcn_readlane(w.v1, ee) - (ce + bm - 1) / bm;
+    WaveTile t;
+    t.e = ee;
+    t.rank0 = (mt - t0) * bm;
+    t.row0 = __builtin_amdgcn_readlane(w.s0, ee) + t.rank0;
+    t.nrows = min(bm, ce - t.rank0);
+    t.hits = __ballot((w.m >> ee) & 1);
+    return t;
 }
 
 }  // namespace mimoe
