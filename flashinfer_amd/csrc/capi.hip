@@ -206,11 +206,11 @@ enum class Front {
 };
 
 // Largest T whose routing every GEMM1 workgroup repeats by default. Each
-// workgroup routes all T tokens before its first weight load, which costs
-// more than the routing launch it saves from T = 2 on (measured per call:
-// T=1 18.9 against 21.7 us, T=2 27.9 against 27.1, T=4 43.9 against 38.6,
-// T=16 119.6 against 89.0).
-constexpr int64_t ROUTE_IN_GEMM1_MAX_T = 1;
+// workgroup routes all T tokens (one per wave) before its first weight load;
+// with 8 workgroup rows at T <= 4 that beats the routing launch it saves up
+// to T = 4 (measured per call on MI355X: T=2 21.0 against 22.4 us, T=4 33.8
+// against 35.5) and loses beyond (T=16 126.8 against 100.4).
+constexpr int64_t ROUTE_IN_GEMM1_MAX_T = 4;
 
 int env_flag(const char* name) {  // -1 unset, else 0 / 1
     const char* v = getenv(name);
