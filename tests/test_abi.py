@@ -206,19 +206,19 @@ def test_python_wrapper_validates_shapes_and_device():
 def test_phase_timing_switch(monkeypatch):
     """Timing is on only with FIB_PROFILE_PHASES=1 and an output path, and only
     until the first file is written (kernel.py:30-35 of the reference)."""
-    monkeypatch.setattr(kernel, "_PHASE_TIMING_EMITTED", False)
+    monkeypatch.setattr(kernel, "_PHASE_JSON_WRITTEN", False)
     monkeypatch.delenv("FIB_PROFILE_PHASES", raising=False)
     monkeypatch.delenv("FIB_PHASE_TIMING_OUTPUT", raising=False)
-    assert not kernel._phase_timing_enabled()
+    assert not kernel._phase_json_wanted()
     monkeypatch.setenv("FIB_PROFILE_PHASES", "1")
-    assert not kernel._phase_timing_enabled()
+    assert not kernel._phase_json_wanted()
     monkeypatch.setenv("FIB_PHASE_TIMING_OUTPUT", "/tmp/x.json")
-    assert kernel._phase_timing_enabled()
+    assert kernel._phase_json_wanted()
     monkeypatch.setenv("FIB_PROFILE_PHASES", "0")
-    assert not kernel._phase_timing_enabled()
+    assert not kernel._phase_json_wanted()
     monkeypatch.setenv("FIB_PROFILE_PHASES", "1")
-    monkeypatch.setattr(kernel, "_PHASE_TIMING_EMITTED", True)
-    assert not kernel._phase_timing_enabled()
+    monkeypatch.setattr(kernel, "_PHASE_JSON_WRITTEN", True)
+    assert not kernel._phase_json_wanted()
 
 
 @pytest.mark.parametrize("shape", [(7168, 2048), (4096, 1536)])
