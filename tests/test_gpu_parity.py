@@ -253,6 +253,37 @@ def test_gemm2_precision_modes_prefill(name, monkeypatch):
         assert e["default"] <= 3.2e-3
 
 
+@pytest.mark.parametrize("T", [2, 3, 4])
+def test_decode_row_loop_many_tiles(T, monkeypatch):
+    """At T <= 4 the GEMM1 front kernel has 8 workgroup rows, each looping
+    over row tiles y, y + 8, .... Logits that send token t to local experts
+    8t .. 8t+7 (zero bias) put every slot on its own expert: 8T one-row tiles,
+    so the rows loop from T = 2. Every token matches the oracle, 8T experts
+    hold a slot, and the output has the bits of the separate routing and sort
+    launches (whose GEMM1 takes one tile per workgroup row)."""
+    from flashinfer_amd import _lib, kernel
+    from oracle import ref_moe as R
+    log(f"test_decode_row_loop_many_tiles[T={T}]")
+    wl = W.make_workload("row_loop", T, 500 + T, local_expert_offset=0)
+    t = wl.tensors
+    t["routing_bias"].zero_()
+    lg = t["routing_logits"]
+    lg.mul_(0.1)
+    for tok in range(T):
+        lg[tok, 8 * tok:8 * tok + 8] = 6.0 + 0.1 * torch.arange(8, dtype=lg.dtype)
+    for k in ("MI_MOE_FUSE_FRONT", "MI_MOE_ROUTE_IN_GEMM1", "MI_MOE_SORT_IN_GEMM1"):
+        monkeypatch.delenv(k, raising=False)
+    out = run_gpu(wl, fill=float("nan")).clone()
+    L = _lib.workspace_layout(T)
+    eoff = kernel.last_workspace()[L.expert_off:L.expert_off + 33 * 4].view(torch.int32).cpu()
+    assert int((eoff[1:] > eoff[:-1]).sum()) == 8 * T and int(eoff[32]) == 8 * T
+    _check_output(wl, out, torch.arange(T))
+    for k in ("MI_MOE_FUSE_FRONT", "MI_MOE_ROUTE_IN_GEMM1", "MI_MOE_SORT_IN_GEMM1"):
+        monkeypatch.setenv(k, "0")
+    ref = run_gpu(wl, fill=float("nan"))
+    assert torch.equal(out.view(torch.int16), ref.view(torch.int16))
+
+
 def test_deterministic_bitwise():
     log("test_deterministic_bitwise")
     wl = W.standard("c2_t1024_o0")
