@@ -225,7 +225,7 @@ int env_flag(const char* name) {  // -1 unset, else 0 / 1
 // cost occupancy).
 int gemm2_mode_for(int64_t T, int g2) {
     if (T > F32_PART_MAX_T) return G2_BF16;
-    const bool tile = g2 == 3 || g2 == 4 || g2 == 18;
+    const bool tile = g2 == 3 || g2 == 4 || g2 == 18 || g2 == 20;
     if (!tile && T <= SPLIT_ACT_MAX_T && env_flag("MI_MOE_SPLIT_ACT") == 1) return G2_SPLIT;
     return env_flag("MI_MOE_F32_PARTIALS") == 0 ? G2_BF16 : G2_F32;
 }
@@ -282,13 +282,18 @@ Variants pick_variants(int64_t T) {
     else if (T <= 128) v = {15, 14};  // the wide GEMM1 folds in the sort from T = 65
     else if (T <= 176) v = {15, 13};  // wide GEMM2 ahead by 3.5 us at T = 192, behind by ~2 at 160
     else if (T <= 256) v = {15, 15};
-    else if (T <= 1536) v = {15, 3};
+    // GEMM2 LDS tile as one software pipeline (variant 20): bitwise equal to
+    // variant 3, per call (one process, three alternating passes) T=1024
+    // 367.6 against 372.7 us, T=1536 299.8 against 305.4, T=2048 336-337
+    // against 343-345, T=3072 448.4 against 454.3, T=8192 level to 7 us
+    // faster; 0.3 % slower at T=14000 with every token on 8 experts.
+    else if (T <= 1536) v = {15, 20};
     // GEMM1 LDS tile as one software pipeline (barriers inside the MFMA
     // stream, weight fragments held in registers): bitwise equal to variant
     // 18 and faster at every T (GEMM1 per launch, one process: T=8192 401-420
     // against 436-509 us, T=14000 skewed 2972 against 3151, T=3072 287
     // against 308); level with the wide kernel at T=2048.
-    else v = {19, 3};
+    else v = {19, 20};
     const char* env = getenv("MI_MOE_VARIANT");
     if (env && *env) {
         int a = -1, b = -1;

@@ -191,10 +191,238 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm2_tile_kernel(Plan p,
     }
 }
 
+
+// The 128 x 256 tile of variant 3 as one software pipeline (variant 20), in
+// the manner of GEMM1's variant 19. Wave (wm, wn) owns rows 64wm .. 64wm+63
+// (4 row tiles of 16) and columns 64wn .. 64wn+63 (4 column tiles). It keeps
+// the k-block's weight fragments, widened to bf16, in registers (64 VGPRs)
+// and streams its activation fragments from LDS one row tile ahead. The two
+// barriers of a k-block sit inside the MFMA stream:
+//   * barrier X after row tile 0: every wave holds its weight fragments of
+//     k-block kb, so that stage's weight region takes the copy of k-block
+//     kb+2 (~1.75 k-blocks to land);
+//   * barrier Y before row tile 3: the copies of kb+1 have landed (vmcnt
+//     leaves only kb+2's weight copies outstanding) and the activation rows of
+//     kb are all read, so the activation region takes kb+2's rows. During row
+//     tile 3 each wave reads kb+1's raw weight fragments and first
+//     activation fragment; the weights are widened at their first use.
+// Per unit (row tile m, column tile n) the four MFMAs of the 128-k block
+// chain from zero and the block scale is applied in fp32 one unit later, the
+// arithmetic of variant 3 (bitwise equal). The routing weights and the
+// tile's weight scales go to LDS by DMA in the prologue, so no load of the
+// compiler's own is pending inside the loop.
+template <int GM, int MODE>
+__global__ __launch_bounds__(512) void gemm2_tile_w_kernel(Plan p, const uint8_t* __restrict__ w2,
+                                                           const float* __restrict__ w2s) {
+    using C = G2Tile<2, 4>;
+    static_assert(C::A_LD == 4 && C::B_LD == 4, "vmcnt(4) leaves one k-block of weight copies");
+    static_assert(IB <= 32, "scales: one lane per k-block and 128-column block");
+    __shared__ __attribute__((aligned(1024))) uint8_t smem[2 * C::STAGE];
+    __shared__ __attribute__((aligned(16))) float w_lds[C::BM];     // routing weights of the rows
+    __shared__ __attribute__((aligned(16))) float s_sb[2][32];      // [128-column block][kb] weight scales
+
+    int e, row0, nrows, nt;
+    if (!tile_coords<C::NT, GM>(p.meta, META_MTILE2, C::BM, e, row0, nrows, nt)) return;
+    e = __builtin_amdgcn_readfirstlane(e);
+    nt = __builtin_amdgcn_readfirstlane(nt);
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int n0 = nt * C::BN;
+
+    uint32_t a_off[C::A_LD], b_off[C::B_LD];
+#pragma unroll
+    for (int i = 0; i < C::A_LD; ++i) {
+        const int row = 4 * (wave * C::A_LD + i) + (lane >> 4);
+        const int c = (lane & 15) ^ swz16(row);
+        a_off[i] = (uint32_t)(row0 + min(row, nrows - 1)) * (I * 2) + c * 16;
+    }
+#pragma unroll
+    for (int i = 0; i < C::B_LD; ++i) {
+        const int row = 8 * (wave * C::B_LD + i) + (lane >> 3);
+        const int c = (lane & 7) ^ swz8(row);
+        b_off[i] = (uint32_t)((e * H + n0 + row) * I + c * 16);
+    }
+    const uint8_t* act = reinterpret_cast<const uint8_t*>(p.act);
+    auto issue_a = [&](int stage, int kb) __attribute__((always_inline)) {
+        uint8_t* s = smem + stage * C::STAGE;
+        const uint8_t* base = act + (size_t)kb * (BLK * 2);
+#pragma unroll
+        for (int i = 0; i < C::A_LD; ++i) g2l16s(base, a_off[i], s + (wave * C::A_LD + i) * 1024);
+    };
+    auto issue_b = [&](int stage, int kb) __attribute__((always_inline)) {
+        uint8_t* s = smem + stage * C::STAGE + C::A_BYTES;
+        const uint8_t* base = w2 + kb * BLK;
+#pragma unroll
+        for (int i = 0; i < C::B_LD; ++i) g2l16s(base, b_off[i], s + (wave * C::B_LD + i) * 1024);
+    };
+
+    // Prologue DMA of the tile's constants: the routing weights of its rows
+    // (waves 0, 1) and the weight scales of its two 128-column blocks (wave 2).
+    if (wave < 2) {
+        const int row = wave * 64 + lane;
+        g2l4s(p.sorted_w, (uint32_t)(row0 + min(row, nrows - 1)) * 4, w_lds + wave * 64);
+    } else if (wave == 2) {
+        // lane l -> s_sb[l / 32][l % 32] (k-blocks past IB repeat the last)
+        const int half = lane >> 5, kb = lane & 31;
+        const uint32_t off = (uint32_t)((((size_t)e * HB + n0 / BLK + half) * IB + min(kb, IB - 1)) * 4);
+        g2l4s(w2s, off, &s_sb[0][0]);
+    }
+    // Prologue copies in the order of the steady state: weights and
+    // activations of k-block 0, weights of 1; then (after the barrier that
+    // plays barrier Y of k-block -1) activations of 1.
+    issue_b(0, 0);
+    issue_a(0, 0);
+    issue_b(1, 1);
+    asm volatile("s_waitcnt vmcnt(4)\n\ts_barrier" ::: "memory");
+    issue_a(1, 1);
+
+    const int wm = wave & 1, wn = wave >> 1;
+    const int r = lane & 15, g = lane >> 4;
+    const bool active = wm * 64 < nrows;  // wave-uniform: rows past the expert only copy
+    if (!active) {
+#pragma unroll 1
+        for (int kb = 0; kb < IB; ++kb) {
+            const int kb2 = min(kb + 2, IB - 1);
+            asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+            issue_b(kb & 1, kb2);
+            asm volatile("s_waitcnt vmcnt(4) lgkmcnt(0)\n\ts_barrier" ::: "memory");
+            issue_a(kb & 1, kb2);
+        }
+        wait_vmem();  // no copy into LDS may be pending when the workgroup ends
+        return;
+    }
+
+    // activation fragment of row tile m (4 x 16 B: k offsets 16g+[0,16) and
+    // 64+16g+[0,16) in bf16 pairs, as variant 3 reads them)
+    auto afrag = [&](const uint8_t* s, int m, v4i (&a)[4]) __attribute__((always_inline)) {
+        const int row = wm * 64 + m * 16 + r;
+        const uint8_t* base = s + row * (BLK * 2);
+        const int sw = swz16(row);
+        a[0] = lds16(base + (((2 * g) ^ sw) << 4));
+        a[1] = lds16(base + (((2 * g + 1) ^ sw) << 4));
+        a[2] = lds16(base + (((8 + 2 * g) ^ sw) << 4));
+        a[3] = lds16(base + (((9 + 2 * g) ^ sw) << 4));
+    };
+    // raw weight fragment of column tile n (16 B at chunk g and at g + 4)
+    auto braw = [&](const uint8_t* s, int n, v4i& lo, v4i& hi) __attribute__((always_inline)) {
+        const int brow = wn * 64 + n * 16 + r;
+        const uint8_t* base = s + C::A_BYTES + brow * BLK;
+        const int sw = swz8(brow);
+        lo = lds16(base + ((g ^ sw) << 4));
+        hi = lds16(base + (((g + 4) ^ sw) << 4));
+    };
+    auto widen = [&](const v4i& lo, const v4i& hi, v4i (&b)[4]) __attribute__((always_inline)) {
+        b[0] = fp8x8_to_bf16x8((uint32_t)lo.x, (uint32_t)lo.y);
+        b[1] = fp8x8_to_bf16x8((uint32_t)lo.z, (uint32_t)lo.w);
+        b[2] = fp8x8_to_bf16x8((uint32_t)hi.x, (uint32_t)hi.y);
+        b[3] = fp8x8_to_bf16x8((uint32_t)hi.z, (uint32_t)hi.w);
+    };
+
+    v4f acc[4][4];
+    const v4f zero = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int m = 0; m < 4; ++m)
+#pragma unroll
+        for (int n = 0; n < 4; ++n) acc[m][n] = zero;
+
+    // k-block 0: raw weight fragments, activation fragments of row tile 0
+    v4i blo[4], bhi[4], bq[4][4], acur[4], anx[4];
+#pragma unroll
+    for (int n = 0; n < 4; ++n) braw(smem, n, blo[n], bhi[n]);
+    afrag(smem, 0, acur);
+    const int sbcol = (wn * 64) / BLK;  // this wave's 128-column block of the tile
+
+#pragma unroll 1
+    for (int kb = 0; kb < IB; ++kb) {
+        const int cur = kb & 1;
+        uint8_t* const sc = smem + cur * C::STAGE;
+        uint8_t* const sn = smem + (cur ^ 1) * C::STAGE;
+        const int kb1 = min(kb + 1, IB - 1), kb2 = min(kb + 2, IB - 1);
+        const float sb = s_sb[sbcol][kb];
+        auto pin_rows = [&](int m0, int m1) __attribute__((always_inline)) {
+#pragma unroll
+            for (int m = m0; m < m1; ++m)
+                asm volatile("" : "+v"(acc[m][0]), "+v"(acc[m][1]), "+v"(acc[m][2]), "+v"(acc[m][3]));
+        };
+        v4f pr[16];
+#pragma unroll
+        for (int u = 0; u < 16; ++u) {
+            const int m = u >> 2, n = u & 3;
+            if (n == 0) asm volatile("" ::: "memory");
+            if (u == 4) {  // barrier X: every wave holds its weight fragments of kb
+                pin_rows(2, 4);
+                asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+                issue_b(cur, kb2);
+            }
+            if (u == 12) {  // barrier Y: kb+1 has landed; activations of kb all read
+                pin_rows(0, 2);
+                asm volatile("s_waitcnt vmcnt(4) lgkmcnt(0)\n\ts_barrier" ::: "memory");
+                issue_a(cur, kb2);
+            }
+            // next row tile's activation fragment (row tile 0 of kb+1 once it has landed)
+            if (n == 0 && m < 3) afrag(sc, m + 1, anx);
+            if (u == 12) afrag(sn, 0, anx);
+            if (m == 0) widen(blo[n], bhi[n], bq[n]);  // weights of kb, widened at their first use
+            v4f t4 = zero;
+            t4 = mfma_bf16_16x16x32(__builtin_bit_cast(v8bf, acur[0]), __builtin_bit_cast(v8bf, bq[n][0]), t4);
+            t4 = mfma_bf16_16x16x32(__builtin_bit_cast(v8bf, acur[1]), __builtin_bit_cast(v8bf, bq[n][1]), t4);
+            t4 = mfma_bf16_16x16x32(__builtin_bit_cast(v8bf, acur[2]), __builtin_bit_cast(v8bf, bq[n][2]), t4);
+            t4 = mfma_bf16_16x16x32(__builtin_bit_cast(v8bf, acur[3]), __builtin_bit_cast(v8bf, bq[n][3]), t4);
+            pr[u] = t4;
+            if (m == 3) braw(sn, n, blo[n], bhi[n]);  // raw weights of kb+1
+            if (n == 3) {
+#pragma unroll
+                for (int h = 0; h < 4; ++h) acur[h] = anx[h];
+            }
+            if (u >= 1) {  // the previous unit's scale-and-accumulate
+                const int pm = (u - 1) >> 2, pn = (u - 1) & 3;
+#pragma unroll
+                for (int v = 0; v < 4; ++v) acc[pm][pn][v] += pr[u - 1][v] * sb;
+            }
+            __builtin_amdgcn_sched_barrier(0);
+        }
+#pragma unroll
+        for (int v = 0; v < 4; ++v) acc[3][3][v] += pr[15][v] * sb;
+        (void)kb1;
+    }
+    wait_vmem();  // no copy into LDS may be pending when the workgroup ends
+
+    // Epilogue: routing weight (kernel.py:364) and a bf16 (MODE G2_BF16) or
+    // fp32 (G2_F32) row for the combine, as variant 3 writes them.
+#pragma unroll
+    for (int m = 0; m < 4; ++m) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int row = wm * 64 + m * 16 + g * 4 + i;
+            if (row < nrows) {
+                const float w = w_lds[row];
+                const size_t o = (size_t)(row0 + row) * H + n0 + wn * 64 + r;
+#pragma unroll
+                for (int n = 0; n < 4; ++n) {
+                    if constexpr (MODE == G2_F32)
+                        p.part_f32[o + n * 16] = w * acc[m][n][i];
+                    else
+                        p.part[o + n * 16] = f2bf(w * acc[m][n][i]);
+                }
+            }
+        }
+    }
+}
+
 hipError_t launch_gemm2_tile(const Plan& p, const uint8_t* w2, const float* w2s, int variant,
                              hipStream_t s) {
     const bool f32 = gemm2_mode(p) != G2_BF16;
-    if (variant == 3 || variant == 18) {
+    if (variant == 20) {
+        using C = G2Tile<2, 4>;
+        const int tiles = max_mtiles(p.T, C::BM) * C::NT;
+        dim3 grid((tiles + 7) / 8 * 8);
+        if (f32)
+            hipLaunchKernelGGL((gemm2_tile_w_kernel<4, G2_F32>), grid, dim3(C::THREADS), 0, s, p, w2, w2s);
+        else
+            hipLaunchKernelGGL((gemm2_tile_w_kernel<4, G2_BF16>), grid, dim3(C::THREADS), 0, s, p, w2, w2s);
+    } else if (variant == 3 || variant == 18) {
         using C = G2Tile<2, 4>;
         const int tiles = max_mtiles(p.T, C::BM) * C::NT;
         dim3 grid((tiles + 7) / 8 * 8);

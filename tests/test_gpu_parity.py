@@ -429,11 +429,12 @@ def test_scalar_tensor_arguments():
     assert torch.equal(a.view(torch.int16), out.view(torch.int16))
 
 
-# Every GEMM1 id (0-9, 11, 12, 15, 16, 18, 19) and every GEMM2 id (0-18) appears at least once.
+# Every GEMM1 id (0-9, 11, 12, 15, 16, 18, 19) and every GEMM2 id (0-18, 20) appears at least once.
 @pytest.mark.parametrize("variant", ["0", "1", "2", "3", "4", "0,3", "3,0", "5,10", "6,6", "7,1",
                                      "8,2", "9,10", "1,10", "11,11", "12,12", "5,13", "5,14",
                                      "2,9", "9,5", "5,7", "5,8", "15", "15,3", "5,15", "16", "16,14",
-                                     "16,17", "18", "18,5", "16,16", "16,9", "19,3", "19,14"])
+                                     "16,17", "18", "18,5", "16,16", "16,9", "19,3", "19,14",
+                                     "15,20", "19,20"])
 @pytest.mark.parametrize("name", ["c1_t64", "t256", "c2_t1024_o128"])
 def test_every_gemm_variant_matches_oracle(name, variant, monkeypatch):
     """Each GEMM kernel family (weight-streaming with 16/32/64-row tiles, LDS
@@ -445,11 +446,12 @@ def test_every_gemm_variant_matches_oracle(name, variant, monkeypatch):
     _check_output(wl, out, spread_tokens(wl.T, 96))
 
 
-@pytest.mark.parametrize("variant", ["15", "15,3", "3,3", "18,3", "19,3"])
+@pytest.mark.parametrize("variant", ["15", "15,3", "3,3", "18,3", "19,3", "19,20"])
 @pytest.mark.parametrize("name", ["c3_t8192", "c4_t14000_skew"])
 def test_wide_variants_large(name, variant, monkeypatch):
-    """The wide kernels and the GEMM1 LDS tiles (variant 3, 18 with swapped
-    operands, 19 with register-held weight fragments) at prefill sizes: many row tiles per expert (T=8192)
+    """The wide kernels and the LDS tiles (GEMM1 variant 3, 18 with swapped
+    operands, 19 with register-held weight fragments; GEMM2 variant 3 and its
+    pipelined form 20) at prefill sizes: many row tiles per expert (T=8192)
     and 14,000 rows on each of 8 experts."""
     log(f"test_wide_variants_large[{name}-{variant}]")
     monkeypatch.setenv("MI_MOE_VARIANT", variant)

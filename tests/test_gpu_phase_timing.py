@@ -22,7 +22,7 @@ def test_phase_timing_json_written_once(tmp_path, monkeypatch):
     out_path = tmp_path / "phases" / "t64.json"
     monkeypatch.setenv("FIB_PROFILE_PHASES", "1")
     monkeypatch.setenv("FIB_PHASE_TIMING_OUTPUT", str(out_path))
-    monkeypatch.setattr(kernel, "_PHASE_TIMING_EMITTED", False)
+    monkeypatch.setattr(kernel, "_PHASE_JSON_WRITTEN", False)
     timed = run_gpu(wl)
     assert torch.equal(timed.view(torch.int16).cpu(), plain.view(torch.int16).cpu())
     d = json.loads(out_path.read_text())
