@@ -157,6 +157,8 @@ Plan make_plan(void* workspace, const mi_moe_layout& L, int64_t T, int64_t local
     p.part = (uint16_t*)(ws + L.part);
     p.part_f32 = nullptr;
     p.act_lo = nullptr;
+    p.g1_alt_bm = 0;
+    p.g1_mtile = META_MTILE1;
     return p;
 }
 
@@ -193,6 +195,7 @@ const Roctx* roctx() {
 // (0..NUM_VARIANTS-1, for tests and tuning).
 struct Variants {
     int g1, g2;
+    int g1_alt = -1;  // >= 0: GEMM1 variant that the device may choose instead of g1
 };
 
 // Which launches do routing and the sort (decode sizes fold them into
@@ -288,6 +291,14 @@ Variants pick_variants(int64_t T) {
     // against 343-345, T=3072 448.4 against 454.3, T=8192 level to 7 us
     // faster; 0.3 % slower at T=14000 with every token on 8 experts.
     else if (T <= 1536) v = {15, 20};
+    // From T = 640 to 1536 the GEMM1 kernel is chosen on the device from the
+    // expert counts (G1_SELECT_EXTRA_TILES): the wide kernel streams an
+    // expert's weights once per 64-row tile, the LDS tile once per 256 rows,
+    // so experts with hundreds of rows favour the tile (T=1024 offset 0 with
+    // 1,966 slots: 337 against 368 us per call) and evenly spread slots the
+    // wide kernel (T=1024 offset 64: 223 against 255). Both are launched; the
+    // one not chosen finds no tiles. MI_MOE_G1_SELECT=0 keeps the wide kernel.
+    if (T >= 640 && T <= 1536 && !kSmallLayer && EL == 32) v.g1_alt = 19;
     // GEMM1 LDS tile as one software pipeline (barriers inside the MFMA
     // stream, weight fragments held in registers): bitwise equal to variant
     // 18 and faster at every T (GEMM1 per launch, one process: T=8192 401-420
@@ -301,7 +312,9 @@ Variants pick_variants(int64_t T) {
         if (n >= 1 && a >= 0 && a < NUM_VARIANTS) v.g1 = a;
         if (n == 2 && b >= 0 && b < NUM_VARIANTS) v.g2 = b;
         else if (n == 1 && a >= 0 && a < NUM_VARIANTS) v.g2 = a;
+        v.g1_alt = -1;  // a forced variant runs as asked
     }
+    if (env_flag("MI_MOE_G1_SELECT") == 0) v.g1_alt = -1;
     return v;
 }
 
@@ -506,6 +519,9 @@ static int run_impl(const mi_moe_args* a, hipStream_t s, hipEvent_t const* ev,
         front = (gemm1_sorts_supported((int)T, var.g1) && env_flag("MI_MOE_SORT_IN_GEMM1") != 0)
                     ? Front::SORT_IN_GEMM1
                     : Front::KERNELS;
+    // the device-side GEMM1 choice needs the sort launch's counts
+    const bool g1_choice = var.g1_alt >= 0 && front == Front::KERNELS;
+    if (g1_choice) p.g1_alt_bm = gemm1_bm(var.g1_alt);
     const FrontArgs fa{a->routing_logits, a->routing_bias, bias_f32, gemm1_bm(var.g1),
                        gemm2_bm(var.g2)};
     mark(0);
@@ -535,6 +551,13 @@ static int run_impl(const mi_moe_args* a, hipStream_t s, hipEvent_t const* ev,
         else
             err = launch_gemm1(p, a->hidden_states, a->hidden_states_scale, a->gemm1_weights,
                                a->gemm1_weights_scale, var.g1, s);
+        if (err == hipSuccess && g1_choice) {
+            // the alternative kernel, on its own row-tile table (empty unless chosen)
+            Plan q = p;
+            q.g1_mtile = META_MTILE1B;
+            err = launch_gemm1(q, a->hidden_states, a->hidden_states_scale, a->gemm1_weights,
+                               a->gemm1_weights_scale, var.g1_alt, s);
+        }
     }
     mark(3);
     const bool fused_ks = var.g2 == VARIANT_GEMM2_COMBINE_KS && gemm2_combine_supported(p.T);

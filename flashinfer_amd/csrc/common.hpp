@@ -100,6 +100,12 @@ struct Plan {
     // act + act_lo, 16 mantissa bits (the reference's fp32 -> TF32 operand
     // keeps 10, kernel.py:272-278).
     uint16_t* act_lo;          // bf16 [TOPK*T, I] or null
+    // GEMM1 kernel chosen on the device from the expert counts (0: off). When
+    // set, the sort also writes the row-tile prefix for tiles of g1_alt_bm rows
+    // (META_MTILE1B) and zeroes the total of the table it does not choose, so
+    // of the two GEMM1 launches only the chosen one finds tiles.
+    int g1_alt_bm;
+    int g1_mtile;              // META_MTILE1 or META_MTILE1B: the LDS-tile GEMM1's row-tile table
 };
 
 // What a GEMM2 kernel reads and writes (template argument, picked per call).
@@ -114,7 +120,18 @@ constexpr int META_STRIDE = EL < 64 ? 64 : 128;  // holds EL + 1 entries
 constexpr int META_EXPERT_OFF = 0;
 constexpr int META_MTILE1 = META_STRIDE;
 constexpr int META_MTILE2 = 2 * META_STRIDE;
-constexpr int META_INTS = 3 * META_STRIDE;
+constexpr int META_MTILE1B = 3 * META_STRIDE;  // GEMM1 row tiles of g1_alt_bm rows
+constexpr int META_G1_SEL = 4 * META_STRIDE;   // 1: the alternative GEMM1 tile was chosen
+constexpr int META_INTS = 4 * META_STRIDE + 64;
+
+// Device-side GEMM1 choice (Plan::g1_alt_bm): the LDS tile of g1_alt_bm rows
+// runs instead of the 64-row wide kernel when the 64-row tiling would stream
+// at least this many expert weight sets beyond one per active expert (sum_e
+// ceil(c_e / 64) - active experts). Measured on 24 batches of T = 384 ...
+// 1536 at four shard offsets (per call, one process, three alternating
+// passes): thresholds of 11 and 12 came within 23.6 us in total of the
+// better kernel on every batch, against 218 us for the wide kernel alone.
+constexpr int G1_SELECT_EXTRA_TILES = 11;
 
 typedef int v4i __attribute__((ext_vector_type(4)));
 typedef int v8i __attribute__((ext_vector_type(8)));

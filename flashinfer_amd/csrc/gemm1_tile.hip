@@ -447,7 +447,7 @@ __global__ __launch_bounds__(512) void gemm1_tile_w_kernel(
     __shared__ __attribute__((aligned(16))) float s_sb[2 * 64];  // [gate | up][kb] weight scales
 
     int e, row0, nrows, nt;
-    if (!tile_coords<C::NT, GM>(p.meta, META_MTILE1, C::BM, e, row0, nrows, nt)) return;
+    if (!tile_coords<C::NT, GM>(p.meta, p.g1_mtile, C::BM, e, row0, nrows, nt)) return;
     // wave-uniform by construction; kept in SGPRs for the copies' scalar bases
     e = __builtin_amdgcn_readfirstlane(e);
     nt = __builtin_amdgcn_readfirstlane(nt);

@@ -55,21 +55,38 @@ __device__ __forceinline__ TokLocal load_local(const int* ids_base, const float*
 // expert offsets and the row-tile prefixes for GEMM tiles of bm1 / bm2 rows.
 __device__ __forceinline__ int scan_counts(const Plan& p, int lane, int c, int bm1, int bm2,
                                            bool write) {
-    int v0 = c, v1 = (c + bm1 - 1) / bm1, v2 = (c + bm2 - 1) / bm2;
-    const int own0 = v0, own1 = v1, own2 = v2;
+    const int bm3 = p.g1_alt_bm > 0 ? p.g1_alt_bm : bm1;
+    int v0 = c, v1 = (c + bm1 - 1) / bm1, v2 = (c + bm2 - 1) / bm2, v3 = (c + bm3 - 1) / bm3;
+    const int own0 = v0, own1 = v1, own2 = v2, own3 = v3;
 #pragma unroll
     for (int d = 1; d < EL; d <<= 1) {
-        const int u0 = __shfl_up(v0, d), u1 = __shfl_up(v1, d), u2 = __shfl_up(v2, d);
-        if (lane >= d) { v0 += u0; v1 += u1; v2 += u2; }
+        const int u0 = __shfl_up(v0, d), u1 = __shfl_up(v1, d), u2 = __shfl_up(v2, d),
+                  u3 = __shfl_up(v3, d);
+        if (lane >= d) { v0 += u0; v1 += u1; v2 += u2; v3 += u3; }
+    }
+    // Device-side GEMM1 choice (uniform: g1_alt_bm is a launch argument):
+    // the alternative tile when the bm1-row tiling has at least
+    // G1_SELECT_EXTRA_TILES more row tiles than active experts.
+    int alt = 0;
+    if (p.g1_alt_bm > 0) {
+        const int active = __popcll(__ballot(lane < EL && c > 0));
+        const int t1 = __shfl(v1, EL - 1);
+        alt = t1 - active >= G1_SELECT_EXTRA_TILES ? 1 : 0;
     }
     if (write && lane < EL) {
         p.meta[META_EXPERT_OFF + lane] = v0 - own0;
         p.meta[META_MTILE1 + lane] = v1 - own1;
         p.meta[META_MTILE2 + lane] = v2 - own2;
+        if (p.g1_alt_bm > 0) p.meta[META_MTILE1B + lane] = v3 - own3;
         if (lane == EL - 1) {
             p.meta[META_EXPERT_OFF + EL] = v0;
-            p.meta[META_MTILE1 + EL] = v1;
             p.meta[META_MTILE2 + EL] = v2;
+            // the table of the kernel not chosen holds no tiles
+            p.meta[META_MTILE1 + EL] = alt ? 0 : v1;
+            if (p.g1_alt_bm > 0) {
+                p.meta[META_MTILE1B + EL] = alt ? v3 : 0;
+                p.meta[META_G1_SEL] = alt;
+            }
         }
     }
     return v0 - own0;

@@ -461,6 +461,42 @@ def test_wide_variants_large(name, variant, monkeypatch):
     _check_output(wl, out, spread_tokens(wl.T, 48))
 
 
+@pytest.mark.parametrize("name,T", [("c2_t1024_o0", 1024), ("c2_t1024_o64", 1024),
+                                    ("c2_t1024_o0", 768), ("c2_t1024_o64", 1280),
+                                    ("c2_t1024_o224", 1280), ("c2_t1024_o128", 1536),
+                                    ("c2_t1024_o0", 640)])
+def test_gemm1_device_choice(name, T, monkeypatch):
+    """From T = 640 to 1536 the sort chooses the GEMM1 kernel from the expert
+    counts: the LDS tile (variant 19) when the 64-row tiling has at least 11
+    more row tiles than active experts, else the wide kernel (15). The chosen
+    kernel's row-tile table holds the tiles and the other one's holds none;
+    the output is bitwise the one either variant gives when forced (both
+    apply the same per-block products in the same fp32 order, so the choice
+    changes only the time), and within the bar of the oracle."""
+    from oracle import ref_moe as R
+    from flashinfer_amd import _lib, kernel
+    log(f"test_gemm1_device_choice[{name}:{T}]")
+    wl = W.standard(name, T=T)
+    r = R.route(wl.tensors["routing_logits"], wl.tensors["routing_bias"], wl.routed_scaling_factor)
+    ids = r.ids.flatten() - wl.local_expert_offset
+    cnt = torch.bincount(ids[(ids >= 0) & (ids < 32)], minlength=32)
+    want = int(((cnt + 63) // 64).sum()) - int((cnt > 0).sum()) >= 11
+    out = run_gpu(wl, fill=float("nan")).clone()
+    L = _lib.workspace_layout(T)
+    meta = kernel.last_workspace()[L.expert_off:L.expert_off + 320 * 4].view(torch.int32).cpu()
+    assert int(meta[256]) == int(want)
+    tiles64, tiles256 = int(((cnt + 63) // 64).sum()), int(((cnt + 255) // 256).sum())
+    assert int(meta[64 + 32]) == (0 if want else tiles64)
+    assert int(meta[192 + 32]) == (tiles256 if want else 0)
+    monkeypatch.setenv("MI_MOE_VARIANT", "19,20" if want else "15,20")
+    forced = run_gpu(wl, fill=float("nan"))
+    assert torch.equal(out.view(torch.int16), forced.view(torch.int16))
+    monkeypatch.setenv("MI_MOE_VARIANT", "15,20" if want else "19,20")
+    other = run_gpu(wl, fill=float("nan"))
+    assert torch.equal(out.view(torch.int16), other.view(torch.int16))
+    _check_output(wl, out, spread_tokens(T, 64))
+
+
 @pytest.mark.parametrize("fuse", ["0", "1"])
 @pytest.mark.parametrize("name", ["c1_t1", "c0_t16", "c1_t64", "t256"])
 def test_front_end_fused_and_split_agree(name, fuse, monkeypatch):
