@@ -284,13 +284,23 @@ Variants pick_variants(int64_t T) {
     else if (kSmallLayer && T * TOPK <= kStreamMaxSlotsPerExpert * EG) v = {16, 14};
     else if (T <= 128) v = {15, 14};  // the wide GEMM1 folds in the sort from T = 65
     else if (T <= 176) v = {15, 13};  // wide GEMM2 ahead by 3.5 us at T = 192, behind by ~2 at 160
-    else if (T <= 256) v = {15, 15};
+    // The wide GEMM2 (32-row tiles) to T = 640, the LDS tile above: per call
+    // (one process, three alternating passes, four shard offsets) the wide
+    // kernel is 6-18 us faster at T = 320, 1-28 at 448 and 512, level on
+    // average at 640, and 10-23 us slower at 768.
+    else if (T <= 640) v = {15, 15};
     // GEMM2 LDS tile as one software pipeline (variant 20): bitwise equal to
     // variant 3, per call (one process, three alternating passes) T=1024
     // 367.6 against 372.7 us, T=1536 299.8 against 305.4, T=2048 336-337
     // against 343-345, T=3072 448.4 against 454.3, T=8192 level to 7 us
     // faster; 0.3 % slower at T=14000 with every token on 8 experts.
     else if (T <= 1536) v = {15, 20};
+    // GEMM1 LDS tile as one software pipeline (barriers inside the MFMA
+    // stream, weight fragments held in registers): bitwise equal to variant
+    // 18 and faster at every T (GEMM1 per launch, one process: T=8192 401-420
+    // against 436-509 us, T=14000 skewed 2972 against 3151, T=3072 287
+    // against 308); level with the wide kernel at T=2048.
+    else v = {19, 20};
     // From T = 640 to 1536 the GEMM1 kernel is chosen on the device from the
     // expert counts (G1_SELECT_EXTRA_TILES): the wide kernel streams an
     // expert's weights once per 64-row tile, the LDS tile once per 256 rows,
@@ -299,12 +309,6 @@ Variants pick_variants(int64_t T) {
     // wide kernel (T=1024 offset 64: 223 against 255). Both are launched; the
     // one not chosen finds no tiles. MI_MOE_G1_SELECT=0 keeps the wide kernel.
     if (T >= 640 && T <= 1536 && !kSmallLayer && EL == 32) v.g1_alt = 19;
-    // GEMM1 LDS tile as one software pipeline (barriers inside the MFMA
-    // stream, weight fragments held in registers): bitwise equal to variant
-    // 18 and faster at every T (GEMM1 per launch, one process: T=8192 401-420
-    // against 436-509 us, T=14000 skewed 2972 against 3151, T=3072 287
-    // against 308); level with the wide kernel at T=2048.
-    else v = {19, 20};
     const char* env = getenv("MI_MOE_VARIANT");
     if (env && *env) {
         int a = -1, b = -1;

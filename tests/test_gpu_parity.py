@@ -461,6 +461,24 @@ def test_wide_variants_large(name, variant, monkeypatch):
     _check_output(wl, out, spread_tokens(wl.T, 48))
 
 
+@pytest.mark.parametrize("name,T,variant", [
+    ("c1_t1_local", 1, "16,17"), ("c1_t4", 4, "16,17"), ("c1_t16", 16, "16,16"),
+    ("c1_t64", 64, "16,14"), ("t256", 128, "15,14"), ("t256", 176, "15,13"), ("t256", 256, "15,15"),
+    ("c2_t1024_o0", 512, "15,15"), ("c2_t1024_o64", 1024, "15,20"), ("c3_t8192", 2048, "19,20")])
+def test_default_variants_by_T(name, T, variant, monkeypatch):
+    """The kernels picked from T (no MI_MOE_VARIANT) are the ones of the
+    selection table: the default call is bitwise the call with that variant
+    pair forced (a forced pair gives other bits: the GEMM2 families sum their
+    k chunks in different orders)."""
+    log(f"test_default_variants_by_T[{name}:{T}-{variant}]")
+    monkeypatch.delenv("MI_MOE_VARIANT", raising=False)
+    wl = W.standard(name, T=T)
+    out = run_gpu(wl, fill=float("nan")).clone()
+    monkeypatch.setenv("MI_MOE_VARIANT", variant)
+    forced = run_gpu(wl, fill=float("nan"))
+    assert torch.equal(out.view(torch.int16), forced.view(torch.int16))
+
+
 @pytest.mark.parametrize("name,T", [("c2_t1024_o0", 1024), ("c2_t1024_o64", 1024),
                                     ("c2_t1024_o0", 768), ("c2_t1024_o64", 1280),
                                     ("c2_t1024_o224", 1280), ("c2_t1024_o128", 1536),
@@ -488,10 +506,11 @@ def test_gemm1_device_choice(name, T, monkeypatch):
     tiles64, tiles256 = int(((cnt + 63) // 64).sum()), int(((cnt + 255) // 256).sum())
     assert int(meta[64 + 32]) == (0 if want else tiles64)
     assert int(meta[192 + 32]) == (tiles256 if want else 0)
-    monkeypatch.setenv("MI_MOE_VARIANT", "19,20" if want else "15,20")
+    g2 = "15" if T <= 640 else "20"  # the default GEMM2 of this T
+    monkeypatch.setenv("MI_MOE_VARIANT", ("19," if want else "15,") + g2)
     forced = run_gpu(wl, fill=float("nan"))
     assert torch.equal(out.view(torch.int16), forced.view(torch.int16))
-    monkeypatch.setenv("MI_MOE_VARIANT", "15,20" if want else "19,20")
+    monkeypatch.setenv("MI_MOE_VARIANT", ("15," if want else "19,") + g2)
     other = run_gpu(wl, fill=float("nan"))
     assert torch.equal(out.view(torch.int16), other.view(torch.int16))
     _check_output(wl, out, spread_tokens(T, 64))
