@@ -87,6 +87,48 @@ def test_graph_capture_and_replay(name, other):
         assert torch.equal(_bits(got), _bits(eager))
 
 
+def test_graph_replay_with_gemm1_choice_flipping():
+    """A captured T=1024 call holds both GEMM1 launches; the sort chooses
+    between them at each replay from that replay's routing. Replays whose
+    routing bias makes the LDS tile win (the captured inputs), then the wide
+    kernel (another bias: fewer rows per expert), then the tile again, each
+    equal the eager call on the same inputs bit for bit, and the eager calls
+    show the choice flipping."""
+    from flashinfer_amd import _lib
+    log("test_graph_replay_with_gemm1_choice_flipping")
+    wl = W.standard("c2_t1024_o0")
+    static = gpu_args(wl)
+    out = torch.empty(wl.T, H, dtype=torch.bfloat16, device="cuda")
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        kernel.run(*static, out)
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        kernel.run(*static, out)
+    torch.cuda.synchronize()
+    bias_tile = wl.tensors["routing_bias"]
+    bias_wide = W.standard_tokens("t256", T=wl.T).tensors["routing_bias"]  # 8 extra 64-row tiles
+    L = _lib.workspace_layout(wl.T)
+    chosen = []
+    for bias in (bias_tile, bias_wide, bias_tile):
+        static[1].copy_(bias)
+        out.fill_(float("nan"))
+        g.replay()
+        torch.cuda.synchronize()
+        got = out.clone()
+        eager = torch.empty_like(out)
+        kernel.run(*static, eager)
+        torch.cuda.synchronize()
+        meta = kernel.last_workspace()[L.expert_off:L.expert_off + 320 * 4].view(torch.int32).cpu()
+        chosen.append(int(meta[256]))
+        assert torch.isfinite(got.float()).all()
+        assert torch.equal(_bits(got), _bits(eager))
+    assert chosen == [1, 0, 1], chosen
+
+
 def test_two_threads_one_stream():
     """Two Python threads calling run on the same stream at once each get
     their own workspace, so interleaved kernels of the two calls cannot mix
