@@ -74,7 +74,12 @@ typedef struct mi_moe_args {
  *   expert_off int32 [E+1]    exclusive prefix of local slot counts (S = [E]),
  *                             followed by the row-tile prefixes of the default
  *                             GEMM kernels at int offsets 64 and 128 (E <= 32)
- *                             or 128 and 256 (E = 64)
+ *                             or 128 and 256 (E = 64); from T = 640 to 1536
+ *                             also the 256-row GEMM1 prefix at 192 and the
+ *                             device's GEMM1 choice at 256 (1: the 256-row
+ *                             tile, whose prefix then holds the tiles; 0: the
+ *                             64-row one, the prefix at 64). The prefix of the
+ *                             kernel not chosen has a total of 0.
  *   sorted_tok int32 [kT]     token of each slot, expert-major, token-ascending
  *   sorted_w   fp32  [kT]     routing weight of each slot
  *   tok_slot   int32 [T, 8]   slots of each token, ascending local expert, -1 pad
