@@ -479,11 +479,13 @@ def test_default_variants_by_T(name, T, variant, monkeypatch):
     assert torch.equal(out.view(torch.int16), forced.view(torch.int16))
 
 
-@pytest.mark.parametrize("name,T", [("c2_t1024_o0", 1024), ("c2_t1024_o64", 1024),
-                                    ("c2_t1024_o0", 768), ("c2_t1024_o64", 1280),
-                                    ("c2_t1024_o224", 1280), ("c2_t1024_o128", 1536),
-                                    ("c2_t1024_o0", 640)])
-def test_gemm1_device_choice(name, T, monkeypatch):
+@pytest.mark.parametrize("name,T,extra", [("c2_t1024_o0", 1024, {}), ("c2_t1024_o64", 1024, {}),
+                                          ("c2_t1024_o0", 768, {}), ("c2_t1024_o64", 1280, {}),
+                                          ("c2_t1024_o224", 1280, {}), ("c2_t1024_o128", 1536, {}),
+                                          ("c2_t1024_o0", 640, {}),
+                                          ("c2_t1024_o0", 1024, {"local_expert_offset": 256}),
+                                          ("c2_t1024_o0", 1024, {"skew": True})])
+def test_gemm1_device_choice(name, T, extra, monkeypatch):
     """From T = 640 to 1536 the sort chooses the GEMM1 kernel from the expert
     counts: the LDS tile (variant 19) when the 64-row tiling has at least 11
     more row tiles than active experts, else the wide kernel (15). The chosen
@@ -493,8 +495,8 @@ def test_gemm1_device_choice(name, T, monkeypatch):
     changes only the time), and within the bar of the oracle."""
     from oracle import ref_moe as R
     from flashinfer_amd import _lib, kernel
-    log(f"test_gemm1_device_choice[{name}:{T}]")
-    wl = W.standard(name, T=T)
+    log(f"test_gemm1_device_choice[{name}:{T}:{extra}]")
+    wl = W.standard(name, T=T, **extra)  # extra: no local token (offset 256), or all on 8 experts
     r = R.route(wl.tensors["routing_logits"], wl.tensors["routing_bias"], wl.routed_scaling_factor)
     ids = r.ids.flatten() - wl.local_expert_offset
     cnt = torch.bincount(ids[(ids >= 0) & (ids < 32)], minlength=32)
