@@ -308,7 +308,11 @@ Variants pick_variants(int64_t T) {
     // 1,966 slots: 337 against 368 us per call) and evenly spread slots the
     // wide kernel (T=1024 offset 64: 223 against 255). Both are launched; the
     // one not chosen finds no tiles. MI_MOE_G1_SELECT=0 keeps the wide kernel.
-    if (T >= 640 && T <= 1536 && !kSmallLayer && EL == 32) v.g1_alt = 19;
+    // The same rule picks the faster kernel with 64 local experts (T = 768 to
+    // 1536: the tile 17-85 us faster at 15-34 extra tiles, the wide kernel 9
+    // us faster at 6); at H = 4096, I = 1536 the wide kernel wins to T = 1536
+    // at up to 18 extra tiles, so smaller layers keep it.
+    if (T >= 640 && T <= 1536 && !kSmallLayer) v.g1_alt = 19;
     const char* env = getenv("MI_MOE_VARIANT");
     if (env && *env) {
         int a = -1, b = -1;

@@ -114,6 +114,36 @@ def test_definition_parity(defn, T):
     _check_output(wl, out, tokens)
 
 
+@pytest.mark.parametrize("T,offset,want", [(768, 0, 0), (768, 128, 1), (1024, 128, 1)])
+def test_ep4_gemm1_device_choice(T, offset, want, monkeypatch):
+    """The default layer with 64 local experts: from T = 640 to 1536 the sort
+    chooses the GEMM1 kernel from the expert counts, as in the 32-expert
+    build (the LDS tile when the 64-row tiling has at least 11 more row tiles
+    than active experts). The choice and both tables are as the oracle's
+    counts give, and the output is bitwise either kernel's forced output and
+    within the bar."""
+    from oracle import ref_moe as R
+    defn = [d for d in DEFS if d.EL == 64][0]
+    log(f"test_ep4_gemm1_device_choice[T={T}-off={offset}]")
+    wl = W.make_for(defn, f"{defn.tag}_choice", T, 900 + T + offset, local_expert_offset=offset)
+    ref = _route_ref(wl, defn)
+    ids = ref.ids.flatten() - offset
+    cnt = torch.bincount(ids[(ids >= 0) & (ids < defn.EL)], minlength=defn.EL)
+    extra = int(((cnt + 63) // 64).sum()) - int((cnt > 0).sum())
+    assert int(extra >= 11) == want  # the batches were picked for each branch
+    out = run_gpu(wl, fill=float("nan")).clone()
+    L = _lib.workspace_layout(T, defn)
+    meta = kernel.last_workspace()[L.expert_off:L.expert_off + 576 * 4].view(torch.int32).cpu()
+    assert int(meta[512]) == want  # stride 128: prefixes at 128 (64-row), 384 (256-row)
+    assert int(meta[128 + 64]) == (0 if want else int(((cnt + 63) // 64).sum()))
+    assert int(meta[384 + 64]) == (int(((cnt + 255) // 256).sum()) if want else 0)
+    for forced in ("15,20", "19,20"):
+        monkeypatch.setenv("MI_MOE_VARIANT", forced)
+        f = run_gpu(wl, fill=float("nan"))
+        assert torch.equal(out.view(torch.int16), f.view(torch.int16)), forced
+    _check_output(wl, out, spread_tokens(T, 48))
+
+
 @pytest.mark.parametrize("defn", DEFS, ids=lambda d: d.tag)
 def test_definition_skewed_batch(defn):
     """Every token's bias makes it pick local experts offset..: each of the top_k
