@@ -339,7 +339,7 @@ __global__ __launch_bounds__(512) void gemm2_tile_w_kernel(Plan p, const uint8_t
         const int cur = kb & 1;
         uint8_t* const sc = smem + cur * C::STAGE;
         uint8_t* const sn = smem + (cur ^ 1) * C::STAGE;
-        const int kb1 = min(kb + 1, IB - 1), kb2 = min(kb + 2, IB - 1);
+        const int kb2 = min(kb + 2, IB - 1);
         const float sb = s_sb[sbcol][kb];
         auto pin_rows = [&](int m0, int m1) __attribute__((always_inline)) {
 #pragma unroll
@@ -385,7 +385,6 @@ __global__ __launch_bounds__(512) void gemm2_tile_w_kernel(Plan p, const uint8_t
         }
 #pragma unroll
         for (int v = 0; v < 4; ++v) acc[3][3][v] += pr[15][v] * sb;
-        (void)kb1;
     }
     wait_vmem();  // no copy into LDS may be pending when the workgroup ends
 
