@@ -19,12 +19,13 @@
 // All loads are ordinary compiler-visible loads, so the compiler's memory
 // counters stay exact and a load waits only for its own data.
 //
-// With SORT (T <= 256) the kernel also stands in for the sort launch: each
-// of its 4 waves ballots one 64-token chunk of the top-k ids per local expert
-// into LDS, every wave derives the expert counts, the bit-plane prefixes and
-// the workgroup's row tile from those ballots, and a row's token is the n-th
-// set bit of its expert's ballot in the right chunk. Workgroup (0, 0) writes
-// the sort's tables for GEMM2 and the combine.
+// With CH > 0 (T <= 64 * CH, CH = 4 up to T = 256, 8 up to 512) the kernel
+// also stands in for the sort launch: its 4 waves ballot the 64-token chunks
+// of the top-k ids (wave w takes chunks w, w + 4, ...) per local expert into LDS, every wave derives the expert
+// counts, the bit-plane prefixes and the workgroup's row tile from those
+// ballots, and a row's token is the n-th set bit of its expert's ballot in
+// the right chunk. Workgroup (0, 0) writes the sort's tables for GEMM2 and
+// the combine.
 //
 // Operand layout as in the stream kernel: lane l feeds row (l % 16) of a
 // 16x128 operand with bytes [32g, 32g+32) of the k-block, g = l / 16 (whole-
@@ -42,7 +43,7 @@ constexpr int WIDE_NW = 4;                  // waves per workgroup
 constexpr int WIDE_G = 16 * WIDE_NW;        // gate columns per workgroup
 constexpr int WIDE_BM = 64;                 // rows per workgroup (see the launcher)
 
-template <int MTW, int D, int DA, bool SORT>
+template <int MTW, int D, int DA, int CH>
 __global__ __launch_bounds__(64 * WIDE_NW) void gemm1_wide_kernel(Plan p, const uint8_t* __restrict__ hs,
                                                                   const float* __restrict__ hs_scale,
                                                                   const uint8_t* __restrict__ w1,
@@ -57,10 +58,12 @@ __global__ __launch_bounds__(64 * WIDE_NW) void gemm1_wide_kernel(Plan p, const 
     __shared__ __attribute__((aligned(16))) uint8_t a_lds[2][BM * BLK];
     __shared__ float sa_lds[HB][BM];  // activation scales of the tile's rows, all k-blocks
     __shared__ __attribute__((aligned(16))) float cs_lds[2][2][BM];  // [buffer][gate, up][row]
-    // SORT: token ballots per (64-token chunk, local expert), and the first
+    // CH > 0: token ballots per (64-token chunk, local expert), and the first
     // slot of each (chunk, expert) for the table writes
-    __shared__ unsigned long long s_bal[SORT ? WIDE_NW : 1][EL];
-    __shared__ int s_base[SORT ? WIDE_NW : 1][EL];
+    constexpr bool SORT = CH > 0;
+    constexpr int CPW = (CH + WIDE_NW - 1) / WIDE_NW;  // chunks per wave
+    __shared__ unsigned long long s_bal[SORT ? CH : 1][EL];
+    __shared__ int s_base[SORT ? CH : 1][EL];
 
     const int tid = threadIdx.x;
     const int lane = tid & 63;
@@ -71,58 +74,68 @@ __global__ __launch_bounds__(64 * WIDE_NW) void gemm1_wide_kernel(Plan p, const 
     int e, row0, nrows, erows;  // erows: the expert's rows over all its row tiles
     int tok_a[A_LD], tok_s;
     if constexpr (SORT) {
-        static_assert(WIDE_NW * 64 >= 256 && BM == 64, "4 chunks of 64 tokens, 64-row tiles");
-        const int t = wave * 64 + lane;
-        emask_t m = 0;
-        if (t < p.T) {
-            int ids[TOPK];
-            load_topk_ids(p.topk_ids + (size_t)t * TOPK_LD, ids);
+        static_assert(BM == 64, "64-row tiles");
+        const int nch = (p.T + 63) >> 6;  // 64-token chunks (T <= 64 * CH)
+        // wave w ballots chunks w, w + WIDE_NW, ...
+        // (with one chunk per wave every wave ballots, tokens past T as zeros)
 #pragma unroll
-            for (int k = 0; k < TOPK; ++k) {
-                const int l = ids[k] - p.local_offset;
-                m |= (unsigned)l < (unsigned)EL ? ebit(l) : (emask_t)0;
+        for (int j = 0; j < CPW; ++j) {
+            const int c = wave + WIDE_NW * j;
+            if (CPW > 1 && c >= nch) break;
+            const int t = c * 64 + lane;
+            emask_t m = 0;
+            if (t < p.T) {
+                int ids[TOPK];
+                load_topk_ids(p.topk_ids + (size_t)t * TOPK_LD, ids);
+#pragma unroll
+                for (int k = 0; k < TOPK; ++k) {
+                    const int l = ids[k] - p.local_offset;
+                    m |= (unsigned)l < (unsigned)EL ? ebit(l) : (emask_t)0;
+                }
+            }
+#pragma unroll
+            for (int x = 0; x < EL; ++x) {
+                const unsigned long long bal = __ballot((m >> x) & 1);
+                if (lane == x) s_bal[c][x] = bal;
             }
         }
-#pragma unroll
-        for (int x = 0; x < EL; ++x) {
-            const unsigned long long bal = __ballot((m >> x) & 1);
-            if (lane == x) s_bal[wave][x] = bal;
-        }
         __syncthreads();
-        // lane x < 32: expert x's count over the chunks; prefixes as in wave_table
-        unsigned long long b[WIDE_NW];
+        // lane x < EL: expert x's count over the chunks; prefixes as in wave_table
         int cnt = 0;
 #pragma unroll
-        for (int c = 0; c < WIDE_NW; ++c) {
-            b[c] = s_bal[c][lane & (EL - 1)];
-            cnt += __popcll(b[c]);
-        }
+        for (int c = 0; c < CH; ++c)
+            cnt += (CPW == 1 || c < nch) ? __popcll(s_bal[c][lane & (EL - 1)]) : 0;
         if (lane >= EL) cnt = 0;
         const int tiles = (cnt + BM - 1) / BM;
-        const int v0 = excl_prefix_small<9>(cnt) + cnt;
+        const int v0 = excl_prefix_small<10>(cnt) + cnt;  // cnt <= T <= 512
         const int v1 = excl_prefix_small(tiles) + tiles;
         if (blockIdx.x == 0 && blockIdx.y == 0) {
             // the sort's tables: expert offsets, both tile prefixes, slots
             const int t2 = (cnt + bm2 - 1) / bm2;
             const int o2 = excl_prefix_small(t2);
-            if (lane < EL) {
-                if (wave == 0) {
-                    p.meta[META_EXPERT_OFF + lane] = v0 - cnt;
-                    p.meta[META_MTILE1 + lane] = v1 - tiles;
-                    p.meta[META_MTILE2 + lane] = o2;
-                    if (lane == EL - 1) {
-                        p.meta[META_EXPERT_OFF + EL] = v0;
-                        p.meta[META_MTILE1 + EL] = v1;
-                        p.meta[META_MTILE2 + EL] = o2 + t2;
-                    }
+            if (lane < EL && wave == 0) {
+                p.meta[META_EXPERT_OFF + lane] = v0 - cnt;
+                p.meta[META_MTILE1 + lane] = v1 - tiles;
+                p.meta[META_MTILE2 + lane] = o2;
+                if (lane == EL - 1) {
+                    p.meta[META_EXPERT_OFF + EL] = v0;
+                    p.meta[META_MTILE1 + EL] = v1;
+                    p.meta[META_MTILE2 + EL] = o2 + t2;
                 }
-                int base = v0 - cnt;
-#pragma unroll
-                for (int c = 0; c < WIDE_NW; ++c) base += c < wave ? __popcll(b[c]) : 0;
-                s_base[wave][lane] = base;
             }
-            const TokLocal tl = load_local(p.topk_ids, p.topk_w, t, t < p.T, p.local_offset);
-            place_with_prefix(p, t, t < p.T, tl, s_base, lane, wave);
+#pragma unroll
+            for (int j = 0; j < CPW; ++j) {
+                const int c = wave + WIDE_NW * j;
+                if (c >= nch) break;
+                if (lane < EL) {  // chunk c's first slot of expert `lane`
+                    int base = v0 - cnt;
+                    for (int c2 = 0; c2 < c; ++c2) base += __popcll(s_bal[c2][lane]);
+                    s_base[c][lane] = base;
+                }
+                const int t = c * 64 + lane;
+                const TokLocal tl = load_local(p.topk_ids, p.topk_w, t, t < p.T, p.local_offset);
+                place_with_prefix(p, t, t < p.T, tl, s_base, lane, c);
+            }
         }
         const int mt = blockIdx.y;
         if (mt >= __builtin_amdgcn_readlane(v1, EL - 1)) return;  // the same for every wave
@@ -135,21 +148,35 @@ __global__ __launch_bounds__(64 * WIDE_NW) void gemm1_wide_kernel(Plan p, const 
         const int rank0 = (mt - tfirst) * BM;
         row0 = sfirst + rank0;
         nrows = min(BM, ce - rank0);
-        unsigned long long eb[WIDE_NW];
+        // token of tile row `row`: the (rank0 + row)-th token of expert ee,
+        // found by walking the chunks' ballots of ee (k < ce, so the walk ends
+        // inside the last chunk at the latest)
+        // (one chunk per wave: the CH ballots held in registers; more: read
+        // from LDS as the walk goes, which keeps scalar registers from spilling)
+        unsigned long long eb[CPW == 1 ? CH : 1];
 #pragma unroll
-        for (int c = 0; c < WIDE_NW; ++c) eb[c] = s_bal[c][ee];
-        // token of tile row `row`: the (rank0 + row)-th token of expert ee
+        for (int c = 0; c < (CPW == 1 ? CH : 1); ++c) eb[c] = s_bal[c][ee];
         auto row_token = [&](int row) __attribute__((always_inline)) {
             int k = rank0 + min(row, nrows - 1);
             int chunk = 0;
             unsigned long long bc = eb[0];
+            if constexpr (CPW == 1) {
 #pragma unroll
-            for (int c = 0; c < WIDE_NW - 1; ++c) {
-                const int cc = __popcll(eb[c]);
-                if (chunk == c && k >= cc) {
+                for (int c = 0; c < CH - 1; ++c) {
+                    const int cc = __popcll(eb[c]);
+                    if (chunk == c && k >= cc) {
+                        k -= cc;
+                        chunk = c + 1;
+                        bc = eb[c + 1];
+                    }
+                }
+            } else {
+                for (int c = 0; c + 1 < nch; ++c) {
+                    const int cc = __popcll(bc);
+                    if (k < cc) break;
                     k -= cc;
                     chunk = c + 1;
-                    bc = eb[c + 1];
+                    bc = s_bal[c + 1][ee];
                 }
             }
             return chunk * 64 + nth_set_bit(bc, k);
@@ -329,13 +356,19 @@ hipError_t launch_gemm1_wide(const Plan& p, const uint8_t* hs, const float* hs_s
     // three waves per SIMD. Measured against 32-, 96- and 128-row tiles and
     // 4- to 8-deep rings, more resident waves beat deeper rings here.
     dim3 grid(I / WIDE_G, max_mtiles(p.T, WIDE_BM));
-    hipLaunchKernelGGL((gemm1_wide_kernel<WIDE_BM / 16, 2, 1, false>), grid, dim3(64 * WIDE_NW), 0, s,
+    hipLaunchKernelGGL((gemm1_wide_kernel<WIDE_BM / 16, 2, 1, 0>), grid, dim3(64 * WIDE_NW), 0, s,
                        p, hs, hs_scale, w1, w1s, 0);
     return hipGetLastError();
 }
 
-// Largest T the sorting wide kernel takes (4 waves x 64 tokens).
-constexpr int WIDE_SORT_MAX_T = 64 * WIDE_NW;
+// Largest T the sorting wide kernel takes: 4 chunks of 64 tokens (one per
+// wave) to T = 256, 8 (two per wave) to T = 512. Per call against the
+// separate sort launch: T=256 220.5 -> 215.9 us, T=200 208.0 -> 202.5, T=160
+// 205.1 -> 199.2 (GEMM1 +1 us, the ~7 us sort launch gone); T=320 176.7 ->
+// 173.7, T=448 260.4 -> 258.2, T=512 182.7 -> 180.4 (four passes, one
+// process per build); at T=576 the separate sort was 2 us faster.
+constexpr int WIDE_SORT_CH_SMALL = 4, WIDE_SORT_CH = 8;
+constexpr int WIDE_SORT_MAX_T = 64 * WIDE_SORT_CH;
 
 bool gemm1_wide_sorts_supported(int T) { return T > 0 && T <= WIDE_SORT_MAX_T; }
 
@@ -344,8 +377,12 @@ hipError_t launch_gemm1_wide_sorting(const Plan& p, const uint8_t* hs, const flo
     if (p.T <= 0) return hipSuccess;
     if (p.T > WIDE_SORT_MAX_T) return hipErrorInvalidValue;
     dim3 grid(I / WIDE_G, max_mtiles(p.T, WIDE_BM));
-    hipLaunchKernelGGL((gemm1_wide_kernel<WIDE_BM / 16, 2, 1, true>), grid, dim3(64 * WIDE_NW), 0, s,
-                       p, hs, hs_scale, w1, w1s, bm2);
+    if (p.T <= 64 * WIDE_SORT_CH_SMALL)
+        hipLaunchKernelGGL((gemm1_wide_kernel<WIDE_BM / 16, 2, 1, WIDE_SORT_CH_SMALL>), grid,
+                           dim3(64 * WIDE_NW), 0, s, p, hs, hs_scale, w1, w1s, bm2);
+    else
+        hipLaunchKernelGGL((gemm1_wide_kernel<WIDE_BM / 16, 2, 1, WIDE_SORT_CH>), grid,
+                           dim3(64 * WIDE_NW), 0, s, p, hs, hs_scale, w1, w1s, bm2);
     return hipGetLastError();
 }
 

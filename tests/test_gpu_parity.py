@@ -548,14 +548,16 @@ def _sort_tables(T):
     (4, 0, False, ""), (9, 0, False, ""), (16, 96, False, ""), (33, 224, False, ""),
     (64, 0, False, ""), (64, 32, True, ""), (48, 256, False, ""), (65, 0, False, ""),
     (100, 32, True, ""), (128, 224, False, ""), (129, 0, False, ""), (200, 96, False, ""),
-    (256, 32, True, ""), (160, 256, False, "")])
+    (256, 32, True, ""), (160, 256, False, ""), (257, 0, False, ""), (300, 64, False, ""),
+    (449, 0, True, ""), (512, 160, False, ""), (511, 32, False, ""), (512, 224, True, ""),
+    (480, 256, False, "")])
 def test_sort_in_gemm1_matches_sort_launch(T, offset, skew, variant, monkeypatch):
     """GEMM1 finding its row tiles from the top-k ids (and writing the sort's
     tables itself) gives bit-identical output and tables to the separate sort
     launch, for every GEMM1 kernel that can do it (K split up to 64, single-
-    wave workgroups when asked for, the wide 64-row tiles from 65 to 256): ragged T,
-    other shard offsets, several row tiles per expert (skew) and no local
-    token at all (offset 256)."""
+    wave workgroups when asked for, the wide 64-row tiles from 65 to 512, up to
+    8 chunks of 64 tokens): ragged T, other shard offsets, several row tiles
+    per expert (skew) and no local token at all (offset 256)."""
     from flashinfer_amd import _lib, kernel
     log(f"test_sort_in_gemm1_matches_sort_launch[T={T}-off={offset}-skew={skew}-v={variant}]")
     wl = W.make_workload("sort_in_gemm1", T, 300 + T, local_expert_offset=offset, skew=skew)
@@ -564,6 +566,7 @@ def test_sort_in_gemm1_matches_sort_launch(T, offset, skew, variant, monkeypatch
     monkeypatch.setenv("MI_MOE_FUSE_FRONT", "0")
     monkeypatch.setenv("MI_MOE_ROUTE_IN_GEMM1", "0")
     monkeypatch.setenv("MI_MOE_SORT_IN_GEMM1", "0")
+    monkeypatch.setenv("MI_MOE_G1_SELECT", "0")  # the plain 64-row table at T = 640
     ref = run_gpu(wl, fill=float("nan")).clone()
     want = _sort_tables(T)
     # scribble over the tables so the second call must rewrite them
