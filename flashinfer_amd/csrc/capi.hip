@@ -6,7 +6,7 @@
 // route -> sort -> GEMM1+SwiGLU -> GEMM2 -> combine on the caller's stream
 // with grids sized from T alone: no device-to-host copy, no host sync
 // (the reference syncs three times, kernel.py:572, :718, :773). Routing and
-// the sort fold into GEMM1 at T = 1, the sort alone up to T = 256 (the
+// the sort fold into GEMM1 up to T = 4, the sort alone up to T = 512 (the
 // stream GEMM1 kernels up to 64, the wide one above); see pick_front.
 #include <dlfcn.h>
 #include <math.h>
