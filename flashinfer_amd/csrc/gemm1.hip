@@ -234,6 +234,27 @@ void gemm1_stream_kernel(Plan p, const uint8_t* __restrict__ hs, const float* __
             }
             return;
         }
+        if (FRONT == FRONT_ROUTE && p.T == 1) {
+            // One token: row tile r is its r-th local expert (slot r, one row),
+            // so the per-wave table (32 ballots and two prefix scans) is not
+            // needed. Per call with two local slots 24.4 against 25.4 us,
+            // bitwise equal.
+            emask_t m = 0;
+#pragma unroll
+            for (int k = 0; k < TOPK; ++k) {
+                const int l = ids_src[k] - p.local_offset;
+                m |= (unsigned)l < (unsigned)EL ? ebit(l) : (emask_t)0;
+            }
+            const int n = epopc(m);
+            for (int mt = row; mt < n; mt += rows) {  // one pass: rows = TOPK at T = 1
+                const int tok[MT] = {0};
+                if (mt != row) __syncthreads();  // the last tile's reads of sa_lds are done
+                int ln = lane;
+                asm volatile("" : "+v"(ln));
+                tile(nth_set_bit((unsigned long long)m, mt), mt, 1, tok, ln, col);
+            }
+            return;
+        }
         const WaveTable tab = wave_table(p, ids_src, lane, BM);
         const int ntiles = table_tiles(tab);
         for (int mt = row; mt < ntiles; mt += rows) {
