@@ -224,7 +224,10 @@ struct WaveTable {
     int v1;        // lane e: inclusive prefix of the row tiles
 };
 
-// ids_base: [T, TOPK_LD], global or LDS. Every lane of the wave calls.
+// ids_base: [T, TOPK_LD], global or LDS. Every lane of the wave calls. Up to
+// SMALL_TABLE_T tokens the expert counts come from the tokens' masks read
+// with readlane instead of one ballot per local expert.
+constexpr int SMALL_TABLE_T = 4;
 __device__ __forceinline__ WaveTable wave_table(const Plan& p, const int* ids_base, int lane, int bm) {
     WaveTable w;
     w.m = 0;
@@ -238,10 +241,26 @@ __device__ __forceinline__ WaveTable wave_table(const Plan& p, const int* ids_ba
         }
     }
     int cnt = 0;
+    if (p.T <= SMALL_TABLE_T) {
+        // a few tokens: lane e counts expert e's bit in each token's mask
 #pragma unroll
-    for (int e = 0; e < EL; ++e) {
-        const unsigned long long bal = __ballot((w.m >> e) & 1);
-        if (lane == e) cnt = __popcll(bal);
+        for (int t = 0; t < SMALL_TABLE_T; ++t) {
+            emask_t mt;
+            if constexpr (EL > 32) {
+                const uint32_t lo = __builtin_amdgcn_readlane((uint32_t)w.m, t);
+                const uint32_t hi = __builtin_amdgcn_readlane((uint32_t)(w.m >> 32), t);
+                mt = ((emask_t)hi << 32) | lo;
+            } else {
+                mt = (emask_t)__builtin_amdgcn_readlane((uint32_t)w.m, t);
+            }
+            cnt += (t < p.T && lane < EL) ? (int)((mt >> (lane & (EL - 1))) & 1) : 0;
+        }
+    } else {
+#pragma unroll
+        for (int e = 0; e < EL; ++e) {
+            const unsigned long long bal = __ballot((w.m >> e) & 1);
+            if (lane == e) cnt = __popcll(bal);
+        }
     }
     const int tiles = (cnt + bm - 1) / bm;
     w.cnt = cnt;
