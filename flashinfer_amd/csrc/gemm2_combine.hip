@@ -56,9 +56,6 @@ __global__ __launch_bounds__(256) void gemm2_combine_kernel(Plan p, const uint8_
     const int nb = n0 / BLK;
     const int r = lane & 15, g = lane >> 4;
 
-    for (int i = tid; i < 4 * T * 16; i += 256) acc_lds[i] = 0.f;
-    __syncthreads();
-
     const int total = p.meta[META_MTILE2 + EL];
     const int nunits = KS > 1 ? total : (wave < total ? (total - wave + 3) / 4 : 0);
     const int nsteps = nunits * KBW;
@@ -66,7 +63,13 @@ __global__ __launch_bounds__(256) void gemm2_combine_kernel(Plan p, const uint8_
     const int u0 = KS > 1 ? 0 : wave;           // a wave's first tile
     const int kb0 = KS > 1 ? wave * KBW : 0;    // a wave's first k-block of each tile
     float* my_acc = acc_lds + wave * T * 16;
+    // Each wave zeroes its own accumulator (no other wave reads it before the
+    // barrier at the end), after its first loads are issued.
+    auto zero_acc = [&]() __attribute__((always_inline)) {
+        for (int i = lane; i < T * 16; i += 64) my_acc[i] = 0.f;
+    };
 
+    if (nsteps <= 0) zero_acc();
     if (nsteps > 0) {
         WRaw b[D];
         v4i a[D][4];
@@ -163,6 +166,7 @@ __global__ __launch_bounds__(256) void gemm2_combine_kernel(Plan p, const uint8_
         fetch_unit(u0);
 #pragma unroll
         for (int d = 0; d < D; ++d) load(d, d);
+        zero_acc();
 #pragma unroll 1
         for (int s0 = 0; s0 < nsteps - D; s0 += D) {
 #pragma unroll
