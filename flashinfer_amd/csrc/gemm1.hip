@@ -207,6 +207,31 @@ void gemm1_stream_kernel(Plan p, const uint8_t* __restrict__ hs, const float* __
         const int row = tables ? 0 : (int)(blockIdx.x - 1) / NCOL;
         const int* ids_src = p.topk_ids;
         const float* w_src = p.topk_w;
+        if (FRONT == FRONT_ROUTE && p.T == 1 && !tables) {
+            // One token: every wave routes it itself (the same result in each,
+            // so no LDS copy and no barrier), and row tile r is its r-th local
+            // expert (slot r, one row), so no per-wave table either. Per call
+            // with two local slots (bitwise equal): 24.4 against 25.4 us for
+            // dropping the table, 23.4 against 24.3 for routing in every wave.
+            int ids[TOPK];
+            float w[TOPK];
+            route_token(fa.logits, fa.bias, fa.bias_is_f32, p.rsf, lane, ids, w);
+            emask_t m = 0;
+#pragma unroll
+            for (int k = 0; k < TOPK; ++k) {
+                const int l = ids[k] - p.local_offset;
+                m |= (unsigned)l < (unsigned)EL ? ebit(l) : (emask_t)0;
+            }
+            const int n = epopc(m);  // the same in every wave of the workgroup
+            for (int mt = row; mt < n; mt += rows) {  // one pass: rows = TOPK at T = 1
+                const int tok[MT] = {0};
+                if (mt != row) __syncthreads();  // the last tile's reads of sa_lds are done
+                int ln = lane;
+                asm volatile("" : "+v"(ln));
+                tile(nth_set_bit((unsigned long long)m, mt), mt, 1, tok, ln, col);
+            }
+            return;
+        }
         if constexpr (FRONT == FRONT_ROUTE) {
             for (int t = wave; t < p.T; t += NWAVES) {
                 int ids[TOPK];
@@ -231,27 +256,6 @@ void gemm1_stream_kernel(Plan p, const uint8_t* __restrict__ hs, const float* __
                     }
                 }
                 sort_one_wave<1>(p, ids_src, w_src, fa.bm1, fa.bm2, lane);
-            }
-            return;
-        }
-        if (FRONT == FRONT_ROUTE && p.T == 1) {
-            // One token: row tile r is its r-th local expert (slot r, one row),
-            // so the per-wave table (32 ballots and two prefix scans) is not
-            // needed. Per call with two local slots 24.4 against 25.4 us,
-            // bitwise equal.
-            emask_t m = 0;
-#pragma unroll
-            for (int k = 0; k < TOPK; ++k) {
-                const int l = ids_src[k] - p.local_offset;
-                m |= (unsigned)l < (unsigned)EL ? ebit(l) : (emask_t)0;
-            }
-            const int n = epopc(m);
-            for (int mt = row; mt < n; mt += rows) {  // one pass: rows = TOPK at T = 1
-                const int tok[MT] = {0};
-                if (mt != row) __syncthreads();  // the last tile's reads of sa_lds are done
-                int ln = lane;
-                asm volatile("" : "+v"(ln));
-                tile(nth_set_bit((unsigned long long)m, mt), mt, 1, tok, ln, col);
             }
             return;
         }
