@@ -228,7 +228,7 @@ int env_flag(const char* name) {  // -1 unset, else 0 / 1
 // cost occupancy).
 int gemm2_mode_for(int64_t T, int g2) {
     if (T > F32_PART_MAX_T) return G2_BF16;
-    const bool tile = g2 == 3 || g2 == 4 || g2 == 18 || g2 == 20;
+    const bool tile = g2 == 3 || g2 == 4 || g2 == 18 || g2 == 20 || g2 == 21;
     if (!tile && T <= SPLIT_ACT_MAX_T && env_flag("MI_MOE_SPLIT_ACT") == 1) return G2_SPLIT;
     return env_flag("MI_MOE_F32_PARTIALS") == 0 ? G2_BF16 : G2_F32;
 }
@@ -293,14 +293,21 @@ Variants pick_variants(int64_t T) {
     // variant 3, per call (one process, three alternating passes) T=1024
     // 367.6 against 372.7 us, T=1536 299.8 against 305.4, T=2048 336-337
     // against 343-345, T=3072 448.4 against 454.3, T=8192 level to 7 us
-    // faster; 0.3 % slower at T=14000 with every token on 8 experts.
-    else if (T <= 1536) v = {15, 20};
+    // faster; 0.3 % slower at T=14000 with every token on 8 experts. The
+    // same kernel run by one workgroup per CU (variant 21), which copies the
+    // next tile's first k-blocks during the last ones of the current tile, is
+    // bitwise equal and faster again (per call, one process, alternating
+    // passes: T=8192 866.3 against 885.6 us, T=14000 skewed 6,633 against
+    // 6,649, T=4096 358.3 against 362.0, T=2048 334.2 against 337.4, T=1536
+    // 419.4 against 422.6, T=1024 364.6 against 370.5 and 221.0 against
+    // 224.1 at two shard offsets).
+    else if (T <= 1536) v = {15, 21};
     // GEMM1 LDS tile as one software pipeline (barriers inside the MFMA
     // stream, weight fragments held in registers): bitwise equal to variant
     // 18 and faster at every T (GEMM1 per launch, one process: T=8192 401-420
     // against 436-509 us, T=14000 skewed 2972 against 3151, T=3072 287
     // against 308); level with the wide kernel at T=2048.
-    else v = {19, 20};
+    else v = {19, 21};
     // From T = 640 to 1536 the GEMM1 kernel is chosen on the device from the
     // expert counts (G1_SELECT_EXTRA_TILES): the wide kernel streams an
     // expert's weights once per 64-row tile, the LDS tile once per 256 rows,

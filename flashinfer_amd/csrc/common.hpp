@@ -423,7 +423,7 @@ hipError_t launch_gemm2_wide(const Plan& p, const uint8_t* w2, const float* w2s,
 // registers so that each weight copy has two k-blocks to arrive.
 // An id without a kernel of its own in one GEMM (9, 10 and 17 for GEMM1, 19
 // for GEMM2) runs that GEMM's default stream shape.
-constexpr int NUM_VARIANTS = 21;
+constexpr int NUM_VARIANTS = 22;
 // GEMM2 variants that also perform the combine (decode sizes only): tiles
 // dealt to the 4 waves, or k-blocks split over them.
 constexpr int VARIANT_GEMM2_COMBINE = 10;

@@ -237,6 +237,7 @@ int gemm2_bm(int variant) {
         case 4: return 64;
         case 18: return 128;
         case 20: return 128;
+        case 21: return 128;
         case 7: return 32;
         case 12: return 32;
         case 15: return 32;
@@ -267,7 +268,7 @@ static void launch_stream2(const Plan& p, const uint8_t* w2, const float* w2s, h
 hipError_t launch_gemm2(const Plan& p, const uint8_t* w2, const float* w2s, int variant,
                         hipStream_t s) {
     if (p.T <= 0) return hipSuccess;
-    if ((variant >= 3 && variant <= 4) || variant == 18 || variant == 20)
+    if ((variant >= 3 && variant <= 4) || variant == 18 || variant == 20 || variant == 21)
         return launch_gemm2_tile(p, w2, w2s, variant, s);
     if (variant == 15) return launch_gemm2_wide(p, w2, w2s, s);
     switch (variant) {

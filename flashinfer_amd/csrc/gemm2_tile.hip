@@ -18,6 +18,9 @@
 // MFMA h uses offsets 16g+8h (h<2) and 64+16g+8(h-2) (h>=2).
 // LDS: weight rows are 128 B with swz8; activation rows are 256 B (16
 // chunks) with chunk c at position c ^ (row & 15).
+#include <algorithm>
+#include <atomic>
+
 #include "tile_common.hpp"
 
 namespace mimoe {
@@ -209,90 +212,109 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm2_tile_kernel(Plan p,
 // Per unit (row tile m, column tile n) the four MFMAs of the 128-k block
 // chain from zero and the block scale is applied in fp32 one unit later, the
 // arithmetic of variant 3 (bitwise equal). The routing weights and the
-// tile's weight scales go to LDS by DMA in the prologue, so no load of the
-// compiler's own is pending inside the loop.
-template <int GM, int MODE>
+// tile's weight scales go to LDS by DMA, so no load of the compiler's own is
+// pending inside the loop.
+//
+// PERSIST (variant 21): one workgroup per CU walks the tiles slot, slot +
+// CPX, ... of its XCD's eighth of the tile order (CPX = workgroups per XCD),
+// and the copy pipeline runs on across tiles: k-steps IB-2 and IB-1 copy the
+// next tile's k-blocks 0 and 1 (and its routing weights and scales, into the
+// other half of two LDS buffers), so the next tile's first copies are in
+// flight during this tile's last MFMAs and its epilogue, instead of starting
+// after a new workgroup is placed and has found its tile.
+template <int GM, int MODE, bool PERSIST>
 __global__ __launch_bounds__(512) void gemm2_tile_w_kernel(Plan p, const uint8_t* __restrict__ w2,
                                                            const float* __restrict__ w2s) {
     using C = G2Tile<2, 4>;
     static_assert(C::A_LD == 4 && C::B_LD == 4, "vmcnt(4) leaves one k-block of weight copies");
     static_assert(IB <= 32, "scales: one lane per k-block and 128-column block");
+    static_assert(IB % 2 == 0, "every tile starts on stage 0");
+    constexpr int NBUF = PERSIST ? 2 : 1;
     __shared__ __attribute__((aligned(1024))) uint8_t smem[2 * C::STAGE];
-    __shared__ __attribute__((aligned(16))) float w_lds[C::BM];     // routing weights of the rows
-    __shared__ __attribute__((aligned(16))) float s_sb[2][32];      // [128-column block][kb] weight scales
+    __shared__ __attribute__((aligned(16))) float w_lds[NBUF][C::BM];  // routing weights of the rows
+    __shared__ __attribute__((aligned(16))) float s_sb[NBUF][2][32];   // [128-column block][kb] weight scales
 
     int e, row0, nrows, nt;
-    if (!tile_coords<C::NT, GM>(p.meta, META_MTILE2, C::BM, e, row0, nrows, nt)) return;
+    int t = 0, t_end = 0, t_step = 0;
+    if constexpr (PERSIST) {
+        const int total = p.meta[META_MTILE2 + EL] * C::NT;
+        const int per_xcd = (total + 7) >> 3;
+        const int t0 = (blockIdx.x & 7) * per_xcd;
+        t_step = gridDim.x >> 3;
+        t = t0 + (blockIdx.x >> 3);
+        t_end = min(total, t0 + per_xcd);
+        if (t >= t_end) return;
+        tile_at<C::NT, GM>(p.meta, META_MTILE2, C::BM, t, e, row0, nrows, nt);
+    } else {
+        if (!tile_coords<C::NT, GM>(p.meta, META_MTILE2, C::BM, e, row0, nrows, nt)) return;
+    }
     e = __builtin_amdgcn_readfirstlane(e);
     nt = __builtin_amdgcn_readfirstlane(nt);
+    row0 = __builtin_amdgcn_readfirstlane(row0);
+    nrows = __builtin_amdgcn_readfirstlane(nrows);
 
     const int tid = threadIdx.x;
     const int lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const int n0 = nt * C::BN;
 
-    uint32_t a_off[C::A_LD], b_off[C::B_LD];
-#pragma unroll
-    for (int i = 0; i < C::A_LD; ++i) {
+    // per-lane copy offsets of a tile (activation rows of its slots, weight
+    // rows of its expert and 256 columns)
+    auto a_offset = [&](int i, int row0_, int nrows_) __attribute__((always_inline)) {
         const int row = 4 * (wave * C::A_LD + i) + (lane >> 4);
         const int c = (lane & 15) ^ swz16(row);
-        a_off[i] = (uint32_t)(row0 + min(row, nrows - 1)) * (I * 2) + c * 16;
-    }
-#pragma unroll
-    for (int i = 0; i < C::B_LD; ++i) {
+        return (uint32_t)(row0_ + min(row, nrows_ - 1)) * (I * 2) + c * 16;
+    };
+    auto b_offset = [&](int i, int e_, int nt_) __attribute__((always_inline)) {
         const int row = 8 * (wave * C::B_LD + i) + (lane >> 3);
         const int c = (lane & 7) ^ swz8(row);
-        b_off[i] = (uint32_t)((e * H + n0 + row) * I + c * 16);
-    }
+        return (uint32_t)((e_ * H + nt_ * C::BN + row) * I + c * 16);
+    };
+    uint32_t a_off[C::A_LD], b_off[C::B_LD];
+#pragma unroll
+    for (int i = 0; i < C::A_LD; ++i) a_off[i] = a_offset(i, row0, nrows);
+#pragma unroll
+    for (int i = 0; i < C::B_LD; ++i) b_off[i] = b_offset(i, e, nt);
     const uint8_t* act = reinterpret_cast<const uint8_t*>(p.act);
-    auto issue_a = [&](int stage, int kb) __attribute__((always_inline)) {
+    auto issue_a = [&](int stage, int kb, const uint32_t* off) __attribute__((always_inline)) {
         uint8_t* s = smem + stage * C::STAGE;
         const uint8_t* base = act + (size_t)kb * (BLK * 2);
 #pragma unroll
-        for (int i = 0; i < C::A_LD; ++i) g2l16s(base, a_off[i], s + (wave * C::A_LD + i) * 1024);
+        for (int i = 0; i < C::A_LD; ++i) g2l16s(base, off[i], s + (wave * C::A_LD + i) * 1024);
     };
-    auto issue_b = [&](int stage, int kb) __attribute__((always_inline)) {
+    auto issue_b = [&](int stage, int kb, const uint32_t* off) __attribute__((always_inline)) {
         uint8_t* s = smem + stage * C::STAGE + C::A_BYTES;
         const uint8_t* base = w2 + kb * BLK;
 #pragma unroll
-        for (int i = 0; i < C::B_LD; ++i) g2l16s(base, b_off[i], s + (wave * C::B_LD + i) * 1024);
+        for (int i = 0; i < C::B_LD; ++i) g2l16s(base, off[i], s + (wave * C::B_LD + i) * 1024);
+    };
+    // DMA of a tile's constants: the routing weights of its rows (waves 0,
+    // 1) and the weight scales of its two 128-column blocks (wave 2).
+    auto consts = [&](int buf, int e_, int row0_, int nrows_, int nt_) __attribute__((always_inline)) {
+        if (wave < 2) {
+            const int row = wave * 64 + lane;
+            g2l4s(p.sorted_w, (uint32_t)(row0_ + min(row, nrows_ - 1)) * 4, &w_lds[buf][wave * 64]);
+        } else if (wave == 2) {
+            // lane l -> s_sb[l / 32][l % 32] (k-blocks past IB repeat the last)
+            const int half = lane >> 5, kb = lane & 31;
+            const uint32_t off =
+                (uint32_t)((((size_t)e_ * HB + nt_ * C::BN / BLK + half) * IB + min(kb, IB - 1)) * 4);
+            g2l4s(w2s, off, &s_sb[buf][0][0]);
+        }
     };
 
-    // Prologue DMA of the tile's constants: the routing weights of its rows
-    // (waves 0, 1) and the weight scales of its two 128-column blocks (wave 2).
-    if (wave < 2) {
-        const int row = wave * 64 + lane;
-        g2l4s(p.sorted_w, (uint32_t)(row0 + min(row, nrows - 1)) * 4, w_lds + wave * 64);
-    } else if (wave == 2) {
-        // lane l -> s_sb[l / 32][l % 32] (k-blocks past IB repeat the last)
-        const int half = lane >> 5, kb = lane & 31;
-        const uint32_t off = (uint32_t)((((size_t)e * HB + n0 / BLK + half) * IB + min(kb, IB - 1)) * 4);
-        g2l4s(w2s, off, &s_sb[0][0]);
-    }
-    // Prologue copies in the order of the steady state: weights and
-    // activations of k-block 0, weights of 1; then (after the barrier that
-    // plays barrier Y of k-block -1) activations of 1.
-    issue_b(0, 0);
-    issue_a(0, 0);
-    issue_b(1, 1);
+    // Prologue copies in the order of the steady state: the tile's
+    // constants, weights and activations of k-block 0, weights of 1; then
+    // (after the barrier that plays barrier Y of k-block -1) activations of 1.
+    consts(0, e, row0, nrows, nt);
+    issue_b(0, 0, b_off);
+    issue_a(0, 0, a_off);
+    issue_b(1, 1, b_off);
     asm volatile("s_waitcnt vmcnt(4)\n\ts_barrier" ::: "memory");
-    issue_a(1, 1);
+    issue_a(1, 1, a_off);
 
     const int wm = wave & 1, wn = wave >> 1;
     const int r = lane & 15, g = lane >> 4;
-    const bool active = wm * 64 < nrows;  // wave-uniform: rows past the expert only copy
-    if (!active) {
-#pragma unroll 1
-        for (int kb = 0; kb < IB; ++kb) {
-            const int kb2 = min(kb + 2, IB - 1);
-            asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
-            issue_b(kb & 1, kb2);
-            asm volatile("s_waitcnt vmcnt(4) lgkmcnt(0)\n\ts_barrier" ::: "memory");
-            issue_a(kb & 1, kb2);
-        }
-        wait_vmem();  // no copy into LDS may be pending when the workgroup ends
-        return;
-    }
+    const int sbcol = (wn * 64) / BLK;  // this wave's 128-column block of the tile
 
     // activation fragment of row tile m (4 x 16 B: k offsets 16g+[0,16) and
     // 64+16g+[0,16) in bf16 pairs, as variant 3 reads them)
@@ -319,95 +341,174 @@ __global__ __launch_bounds__(512) void gemm2_tile_w_kernel(Plan p, const uint8_t
         b[2] = fp8x8_to_bf16x8((uint32_t)hi.x, (uint32_t)hi.y);
         b[3] = fp8x8_to_bf16x8((uint32_t)hi.z, (uint32_t)hi.w);
     };
-
-    v4f acc[4][4];
     const v4f zero = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-    for (int m = 0; m < 4; ++m)
-#pragma unroll
-        for (int n = 0; n < 4; ++n) acc[m][n] = zero;
 
-    // k-block 0: raw weight fragments, activation fragments of row tile 0
-    v4i blo[4], bhi[4], bq[4][4], acur[4], anx[4];
+    int buf = 0;
+    for (;;) {
+        // the next tile of this workgroup, if any
+        bool has_next = false;
+        int en = 0, row0n = 0, nrowsn = 1, ntn = 0;
+        if constexpr (PERSIST) {
+            has_next = t + t_step < t_end;
+            if (has_next) {
+                tile_at<C::NT, GM>(p.meta, META_MTILE2, C::BM, t + t_step, en, row0n, nrowsn, ntn);
+                en = __builtin_amdgcn_readfirstlane(en);
+                row0n = __builtin_amdgcn_readfirstlane(row0n);
+                nrowsn = __builtin_amdgcn_readfirstlane(nrowsn);
+                ntn = __builtin_amdgcn_readfirstlane(ntn);
+            }
+        }
+        // The copies of k-step kb: at barrier X the weights of step kb + 2,
+        // at barrier Y its activations. Step kb + 2 is k-block kb + 2 of this
+        // tile, k-block kb + 2 - IB of the next one, or (no next tile) a
+        // repeat of the last k-block into a stage that is not read again.
+        auto copy_x = [&](int stage, int kb) __attribute__((always_inline)) {
+            if (PERSIST && has_next && kb + 2 >= IB) {
+                if (kb + 2 == IB) consts(buf ^ 1, en, row0n, nrowsn, ntn);
+                uint32_t o[C::B_LD];
 #pragma unroll
-    for (int n = 0; n < 4; ++n) braw(smem, n, blo[n], bhi[n]);
-    afrag(smem, 0, acur);
-    const int sbcol = (wn * 64) / BLK;  // this wave's 128-column block of the tile
+                for (int i = 0; i < C::B_LD; ++i) o[i] = b_offset(i, en, ntn);
+                issue_b(stage, kb + 2 - IB, o);
+            } else {
+                issue_b(stage, min(kb + 2, IB - 1), b_off);
+            }
+        };
+        auto copy_y = [&](int stage, int kb) __attribute__((always_inline)) {
+            if (PERSIST && has_next && kb + 2 >= IB) {
+                uint32_t o[C::A_LD];
+#pragma unroll
+                for (int i = 0; i < C::A_LD; ++i) o[i] = a_offset(i, row0n, nrowsn);
+                issue_a(stage, kb + 2 - IB, o);
+            } else {
+                issue_a(stage, min(kb + 2, IB - 1), a_off);
+            }
+        };
+
+        if (wm * 64 >= nrows) {
+            // Rows past the expert (wave-uniform): copies and barriers only, in
+            // step with the other waves (two barriers per k-block).
+#pragma unroll 1
+            for (int kb = 0; kb < IB; ++kb) {
+                asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+                copy_x(kb & 1, kb);
+                asm volatile("s_waitcnt vmcnt(4) lgkmcnt(0)\n\ts_barrier" ::: "memory");
+                copy_y(kb & 1, kb);
+            }
+        } else {
+            v4f acc[4][4];
+#pragma unroll
+            for (int m = 0; m < 4; ++m)
+#pragma unroll
+                for (int n = 0; n < 4; ++n) acc[m][n] = zero;
+
+            // k-block 0: raw weight fragments, activation fragments of row tile 0
+            v4i blo[4], bhi[4], bq[4][4], acur[4], anx[4];
+#pragma unroll
+            for (int n = 0; n < 4; ++n) braw(smem, n, blo[n], bhi[n]);
+            afrag(smem, 0, acur);
 
 #pragma unroll 1
-    for (int kb = 0; kb < IB; ++kb) {
-        const int cur = kb & 1;
-        uint8_t* const sc = smem + cur * C::STAGE;
-        uint8_t* const sn = smem + (cur ^ 1) * C::STAGE;
-        const int kb2 = min(kb + 2, IB - 1);
-        const float sb = s_sb[sbcol][kb];
-        auto pin_rows = [&](int m0, int m1) __attribute__((always_inline)) {
+            for (int kb = 0; kb < IB; ++kb) {
+                const int cur = kb & 1;
+                uint8_t* const sc = smem + cur * C::STAGE;
+                uint8_t* const sn = smem + (cur ^ 1) * C::STAGE;
+                const float sb = s_sb[buf][sbcol][kb];
+                auto pin_rows = [&](int m0, int m1) __attribute__((always_inline)) {
 #pragma unroll
-            for (int m = m0; m < m1; ++m)
-                asm volatile("" : "+v"(acc[m][0]), "+v"(acc[m][1]), "+v"(acc[m][2]), "+v"(acc[m][3]));
-        };
-        v4f pr[16];
+                    for (int m = m0; m < m1; ++m)
+                        asm volatile("" : "+v"(acc[m][0]), "+v"(acc[m][1]), "+v"(acc[m][2]), "+v"(acc[m][3]));
+                };
+                v4f pr[16];
 #pragma unroll
-        for (int u = 0; u < 16; ++u) {
-            const int m = u >> 2, n = u & 3;
-            if (n == 0) asm volatile("" ::: "memory");
-            if (u == 4) {  // barrier X: every wave holds its weight fragments of kb
-                pin_rows(2, 4);
-                asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
-                issue_b(cur, kb2);
+                for (int u = 0; u < 16; ++u) {
+                    const int m = u >> 2, n = u & 3;
+                    if (n == 0) asm volatile("" ::: "memory");
+                    if (u == 4) {  // barrier X: every wave holds its weight fragments of kb
+                        pin_rows(2, 4);
+                        asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+                        copy_x(cur, kb);
+                    }
+                    if (u == 12) {  // barrier Y: kb+1 has landed; activations of kb all read
+                        pin_rows(0, 2);
+                        asm volatile("s_waitcnt vmcnt(4) lgkmcnt(0)\n\ts_barrier" ::: "memory");
+                        copy_y(cur, kb);
+                    }
+                    // next row tile's activation fragment (row tile 0 of kb+1 once it has landed)
+                    if (n == 0 && m < 3) afrag(sc, m + 1, anx);
+                    if (u == 12) afrag(sn, 0, anx);
+                    if (m == 0) widen(blo[n], bhi[n], bq[n]);  // weights of kb, widened at their first use
+                    v4f t4 = zero;
+                    t4 = mfma_bf16_16x16x32(__builtin_bit_cast(v8bf, acur[0]), __builtin_bit_cast(v8bf, bq[n][0]), t4);
+                    t4 = mfma_bf16_16x16x32(__builtin_bit_cast(v8bf, acur[1]), __builtin_bit_cast(v8bf, bq[n][1]), t4);
+                    t4 = mfma_bf16_16x16x32(__builtin_bit_cast(v8bf, acur[2]), __builtin_bit_cast(v8bf, bq[n][2]), t4);
+                    t4 = mfma_bf16_16x16x32(__builtin_bit_cast(v8bf, acur[3]), __builtin_bit_cast(v8bf, bq[n][3]), t4);
+                    pr[u] = t4;
+                    if (m == 3) braw(sn, n, blo[n], bhi[n]);  // raw weights of kb+1
+                    if (n == 3) {
+#pragma unroll
+                        for (int h = 0; h < 4; ++h) acur[h] = anx[h];
+                    }
+                    if (u >= 1) {  // the previous unit's scale-and-accumulate
+                        const int pm = (u - 1) >> 2, pn = (u - 1) & 3;
+#pragma unroll
+                        for (int v = 0; v < 4; ++v) acc[pm][pn][v] += pr[u - 1][v] * sb;
+                    }
+                    __builtin_amdgcn_sched_barrier(0);
+                }
+#pragma unroll
+                for (int v = 0; v < 4; ++v) acc[3][3][v] += pr[15][v] * sb;
             }
-            if (u == 12) {  // barrier Y: kb+1 has landed; activations of kb all read
-                pin_rows(0, 2);
-                asm volatile("s_waitcnt vmcnt(4) lgkmcnt(0)\n\ts_barrier" ::: "memory");
-                issue_a(cur, kb2);
-            }
-            // next row tile's activation fragment (row tile 0 of kb+1 once it has landed)
-            if (n == 0 && m < 3) afrag(sc, m + 1, anx);
-            if (u == 12) afrag(sn, 0, anx);
-            if (m == 0) widen(blo[n], bhi[n], bq[n]);  // weights of kb, widened at their first use
-            v4f t4 = zero;
-            t4 = mfma_bf16_16x16x32(__builtin_bit_cast(v8bf, acur[0]), __builtin_bit_cast(v8bf, bq[n][0]), t4);
-            t4 = mfma_bf16_16x16x32(__builtin_bit_cast(v8bf, acur[1]), __builtin_bit_cast(v8bf, bq[n][1]), t4);
-            t4 = mfma_bf16_16x16x32(__builtin_bit_cast(v8bf, acur[2]), __builtin_bit_cast(v8bf, bq[n][2]), t4);
-            t4 = mfma_bf16_16x16x32(__builtin_bit_cast(v8bf, acur[3]), __builtin_bit_cast(v8bf, bq[n][3]), t4);
-            pr[u] = t4;
-            if (m == 3) braw(sn, n, blo[n], bhi[n]);  // raw weights of kb+1
-            if (n == 3) {
-#pragma unroll
-                for (int h = 0; h < 4; ++h) acur[h] = anx[h];
-            }
-            if (u >= 1) {  // the previous unit's scale-and-accumulate
-                const int pm = (u - 1) >> 2, pn = (u - 1) & 3;
-#pragma unroll
-                for (int v = 0; v < 4; ++v) acc[pm][pn][v] += pr[u - 1][v] * sb;
-            }
-            __builtin_amdgcn_sched_barrier(0);
-        }
-#pragma unroll
-        for (int v = 0; v < 4; ++v) acc[3][3][v] += pr[15][v] * sb;
-    }
-    wait_vmem();  // no copy into LDS may be pending when the workgroup ends
 
-    // Epilogue: routing weight (kernel.py:364) and a bf16 (MODE G2_BF16) or
-    // fp32 (G2_F32) row for the combine, as variant 3 writes them.
+            // Epilogue: routing weight (kernel.py:364) and a bf16 (MODE G2_BF16) or
+            // fp32 (G2_F32) row for the combine, as variant 3 writes them.
+            const int n0 = nt * C::BN;
 #pragma unroll
-    for (int m = 0; m < 4; ++m) {
+            for (int m = 0; m < 4; ++m) {
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const int row = wm * 64 + m * 16 + g * 4 + i;
-            if (row < nrows) {
-                const float w = w_lds[row];
-                const size_t o = (size_t)(row0 + row) * H + n0 + wn * 64 + r;
+                for (int i = 0; i < 4; ++i) {
+                    const int row = wm * 64 + m * 16 + g * 4 + i;
+                    if (row < nrows) {
+                        const float w = w_lds[buf][row];
+                        const size_t o = (size_t)(row0 + row) * H + n0 + wn * 64 + r;
 #pragma unroll
-                for (int n = 0; n < 4; ++n) {
-                    if constexpr (MODE == G2_F32)
-                        p.part_f32[o + n * 16] = w * acc[m][n][i];
-                    else
-                        p.part[o + n * 16] = f2bf(w * acc[m][n][i]);
+                        for (int n = 0; n < 4; ++n) {
+                            if constexpr (MODE == G2_F32)
+                                p.part_f32[o + n * 16] = w * acc[m][n][i];
+                            else
+                                p.part[o + n * 16] = f2bf(w * acc[m][n][i]);
+                        }
+                    }
                 }
             }
         }
+        if (!PERSIST || !has_next) break;
+        t += t_step;
+        e = en;
+        row0 = row0n;
+        nrows = nrowsn;
+        nt = ntn;
+        buf ^= 1;
+#pragma unroll
+        for (int i = 0; i < C::A_LD; ++i) a_off[i] = a_offset(i, row0, nrows);
+#pragma unroll
+        for (int i = 0; i < C::B_LD; ++i) b_off[i] = b_offset(i, e, nt);
     }
+    wait_vmem();  // no copy into LDS may be pending when the workgroup ends
+}
+
+// Workgroups of the persistent variant: one per CU, a multiple of the 8 XCDs.
+static int persistent_grid() {
+    static std::atomic<int> cache[64];
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) dev = 0;
+    int n = cache[dev].load(std::memory_order_relaxed);
+    if (n == 0) {
+        if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n < 8)
+            n = 256;
+        n = n / 8 * 8;
+        cache[dev].store(n, std::memory_order_relaxed);
+    }
+    return n;
 }
 
 hipError_t launch_gemm2_tile(const Plan& p, const uint8_t* w2, const float* w2s, int variant,
@@ -418,9 +519,17 @@ hipError_t launch_gemm2_tile(const Plan& p, const uint8_t* w2, const float* w2s,
         const int tiles = max_mtiles(p.T, C::BM) * C::NT;
         dim3 grid((tiles + 7) / 8 * 8);
         if (f32)
-            hipLaunchKernelGGL((gemm2_tile_w_kernel<4, G2_F32>), grid, dim3(C::THREADS), 0, s, p, w2, w2s);
+            hipLaunchKernelGGL((gemm2_tile_w_kernel<4, G2_F32, false>), grid, dim3(C::THREADS), 0, s, p, w2, w2s);
         else
-            hipLaunchKernelGGL((gemm2_tile_w_kernel<4, G2_BF16>), grid, dim3(C::THREADS), 0, s, p, w2, w2s);
+            hipLaunchKernelGGL((gemm2_tile_w_kernel<4, G2_BF16, false>), grid, dim3(C::THREADS), 0, s, p, w2, w2s);
+    } else if (variant == 21) {
+        using C = G2Tile<2, 4>;
+        const int tiles = (max_mtiles(p.T, C::BM) * C::NT + 7) / 8 * 8;
+        dim3 grid(std::min(tiles, persistent_grid()));
+        if (f32)
+            hipLaunchKernelGGL((gemm2_tile_w_kernel<4, G2_F32, true>), grid, dim3(C::THREADS), 0, s, p, w2, w2s);
+        else
+            hipLaunchKernelGGL((gemm2_tile_w_kernel<4, G2_BF16, true>), grid, dim3(C::THREADS), 0, s, p, w2, w2s);
     } else if (variant == 3 || variant == 18) {
         using C = G2Tile<2, 4>;
         const int tiles = max_mtiles(p.T, C::BM) * C::NT;

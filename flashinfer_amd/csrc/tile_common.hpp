@@ -77,16 +77,10 @@ __device__ __forceinline__ v4i lds16(const uint8_t* p) { return *reinterpret_cas
 // with the GM row tiles innermost, so the tiles running at the same time
 // on one XCD share weight and activation tiles in that XCD's L2. Each XCD
 // (workgroup b runs on XCD b % 8) takes one contiguous eighth of the order.
+// tile_at returns the coordinates of logical tile t < total.
 template <int NT, int GM>
-__device__ __forceinline__ bool tile_coords(const int* meta, int mtile_base, int bm, int& e,
-                                            int& row0, int& nrows, int& nt) {
-    const int total = meta[mtile_base + EL] * NT;
-    const int per_xcd = (total + 7) >> 3;
-    const int b = blockIdx.x;
-    const int idx = b >> 3;
-    if (idx >= per_xcd) return false;
-    const int t = (b & 7) * per_xcd + idx;
-    if (t >= total) return false;
+__device__ __forceinline__ void tile_at(const int* meta, int mtile_base, int bm, int t, int& e,
+                                        int& row0, int& nrows, int& nt) {
     const int mt = t / NT;  // NT tiles per row tile: find the expert by row-tile index
     int ee = 0;
 #pragma unroll
@@ -102,6 +96,20 @@ __device__ __forceinline__ bool tile_coords(const int* meta, int mtile_base, int
     const int mtl = grp * GM + (v - nt * gm);
     row0 = meta[META_EXPERT_OFF + ee] + mtl * bm;
     nrows = min(bm, meta[META_EXPERT_OFF + ee + 1] - row0);
+}
+
+// The tile of workgroup blockIdx.x in a grid of one workgroup per tile.
+template <int NT, int GM>
+__device__ __forceinline__ bool tile_coords(const int* meta, int mtile_base, int bm, int& e,
+                                            int& row0, int& nrows, int& nt) {
+    const int total = meta[mtile_base + EL] * NT;
+    const int per_xcd = (total + 7) >> 3;
+    const int b = blockIdx.x;
+    const int idx = b >> 3;
+    if (idx >= per_xcd) return false;
+    const int t = (b & 7) * per_xcd + idx;
+    if (t >= total) return false;
+    tile_at<NT, GM>(meta, mtile_base, bm, t, e, row0, nrows, nt);
     return true;
 }
 

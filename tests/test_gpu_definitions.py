@@ -137,7 +137,7 @@ def test_ep4_gemm1_device_choice(T, offset, want, monkeypatch):
     assert int(meta[512]) == want  # stride 128: prefixes at 128 (64-row), 384 (256-row)
     assert int(meta[128 + 64]) == (0 if want else int(((cnt + 63) // 64).sum()))
     assert int(meta[384 + 64]) == (int(((cnt + 255) // 256).sum()) if want else 0)
-    for forced in ("15,20", "19,20"):
+    for forced in ("15,21", "19,21"):
         monkeypatch.setenv("MI_MOE_VARIANT", forced)
         f = run_gpu(wl, fill=float("nan"))
         assert torch.equal(out.view(torch.int16), f.view(torch.int16)), forced

@@ -429,12 +429,12 @@ def test_scalar_tensor_arguments():
     assert torch.equal(a.view(torch.int16), out.view(torch.int16))
 
 
-# Every GEMM1 id (0-9, 11, 12, 15, 16, 18, 19) and every GEMM2 id (0-18, 20) appears at least once.
+# Every GEMM1 id (0-9, 11, 12, 15, 16, 18, 19) and every GEMM2 id (0-18, 20, 21) appears at least once.
 @pytest.mark.parametrize("variant", ["0", "1", "2", "3", "4", "0,3", "3,0", "5,10", "6,6", "7,1",
                                      "8,2", "9,10", "1,10", "11,11", "12,12", "5,13", "5,14",
                                      "2,9", "9,5", "5,7", "5,8", "15", "15,3", "5,15", "16", "16,14",
                                      "16,17", "18", "18,5", "16,16", "16,9", "19,3", "19,14",
-                                     "15,20", "19,20"])
+                                     "15,20", "19,20", "15,21", "19,21"])
 @pytest.mark.parametrize("name", ["c1_t64", "t256", "c2_t1024_o128"])
 def test_every_gemm_variant_matches_oracle(name, variant, monkeypatch):
     """Each GEMM kernel family (weight-streaming with 16/32/64-row tiles, LDS
@@ -446,12 +446,12 @@ def test_every_gemm_variant_matches_oracle(name, variant, monkeypatch):
     _check_output(wl, out, spread_tokens(wl.T, 96))
 
 
-@pytest.mark.parametrize("variant", ["15", "15,3", "3,3", "18,3", "19,3", "19,20"])
+@pytest.mark.parametrize("variant", ["15", "15,3", "3,3", "18,3", "19,3", "19,20", "19,21"])
 @pytest.mark.parametrize("name", ["c3_t8192", "c4_t14000_skew"])
 def test_wide_variants_large(name, variant, monkeypatch):
     """The wide kernels and the LDS tiles (GEMM1 variant 3, 18 with swapped
-    operands, 19 with register-held weight fragments; GEMM2 variant 3 and its
-    pipelined form 20) at prefill sizes: many row tiles per expert (T=8192)
+    operands, 19 with register-held weight fragments; GEMM2 variant 3, its
+    pipelined form 20 and that form run by one workgroup per CU, 21) at prefill sizes: many row tiles per expert (T=8192)
     and 14,000 rows on each of 8 experts."""
     log(f"test_wide_variants_large[{name}-{variant}]")
     monkeypatch.setenv("MI_MOE_VARIANT", variant)
@@ -464,7 +464,7 @@ def test_wide_variants_large(name, variant, monkeypatch):
 @pytest.mark.parametrize("name,T,variant", [
     ("c1_t1_local", 1, "16,17"), ("c1_t4", 4, "16,17"), ("c1_t16", 16, "16,16"),
     ("c1_t64", 64, "16,14"), ("t256", 128, "15,14"), ("t256", 176, "15,13"), ("t256", 256, "15,15"),
-    ("c2_t1024_o0", 512, "15,15"), ("c2_t1024_o64", 1024, "15,20"), ("c3_t8192", 2048, "19,20")])
+    ("c2_t1024_o0", 512, "15,15"), ("c2_t1024_o64", 1024, "15,21"), ("c3_t8192", 2048, "19,21")])
 def test_default_variants_by_T(name, T, variant, monkeypatch):
     """The kernels picked from T (no MI_MOE_VARIANT) are the ones of the
     selection table: the default call is bitwise the call with that variant
@@ -508,7 +508,7 @@ def test_gemm1_device_choice(name, T, extra, monkeypatch):
     tiles64, tiles256 = int(((cnt + 63) // 64).sum()), int(((cnt + 255) // 256).sum())
     assert int(meta[64 + 32]) == (0 if want else tiles64)
     assert int(meta[192 + 32]) == (tiles256 if want else 0)
-    g2 = "15" if T <= 640 else "20"  # the default GEMM2 of this T
+    g2 = "15" if T <= 640 else "21"  # the default GEMM2 of this T
     monkeypatch.setenv("MI_MOE_VARIANT", ("19," if want else "15,") + g2)
     forced = run_gpu(wl, fill=float("nan"))
     assert torch.equal(out.view(torch.int16), forced.view(torch.int16))

@@ -53,7 +53,7 @@ def test_default_kernels_second_shape(T, offset):
 # every kernel family forced, including GEMM2 rings deeper than I/128 = 12
 # k-blocks allow (variants 8 and 11 fall back to 2 deep)
 @pytest.mark.parametrize("variant", ["0", "1", "2", "3", "4", "5,10", "6,6", "7,7", "8,8", "11,11",
-                                     "12,12", "9,13", "16,14", "15", "15,3", "19,20"])
+                                     "12,12", "9,13", "16,14", "15", "15,3", "19,20", "19,21"])
 def test_every_variant_second_shape(variant, monkeypatch):
     log(f"test_every_variant_second_shape[{variant}]")
     monkeypatch.setenv("MI_MOE_VARIANT", variant)
