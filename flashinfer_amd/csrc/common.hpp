@@ -432,5 +432,8 @@ constexpr int VARIANT_GEMM2_COMBINE_KS = 17;
 // Row-tile height of each GEMM variant (rows of one expert per workgroup).
 int gemm1_bm(int variant);
 int gemm2_bm(int variant);
+// Workgroups of the tile kernels that walk their tiles one workgroup per CU:
+// the current device's CU count (a multiple of its 8 XCDs).
+int persistent_grid();
 
 }  // namespace mimoe

@@ -290,6 +290,7 @@ __global__ __launch_bounds__(512) void gemm2_tile_w_kernel(Plan p, const uint8_t
     // DMA of a tile's constants: the routing weights of its rows (waves 0,
     // 1) and the weight scales of its two 128-column blocks (wave 2).
     auto consts = [&](int buf, int e_, int row0_, int nrows_, int nt_) __attribute__((always_inline)) {
+        buf = __builtin_amdgcn_readfirstlane(buf);  // the LDS base goes to M0
         if (wave < 2) {
             const int row = wave * 64 + lane;
             g2l4s(p.sorted_w, (uint32_t)(row0_ + min(row, nrows_ - 1)) * 4, &w_lds[buf][wave * 64]);
@@ -362,26 +363,25 @@ __global__ __launch_bounds__(512) void gemm2_tile_w_kernel(Plan p, const uint8_t
         // at barrier Y its activations. Step kb + 2 is k-block kb + 2 of this
         // tile, k-block kb + 2 - IB of the next one, or (no next tile) a
         // repeat of the last k-block into a stage that is not read again.
+        // The copy offsets switch to the next tile at step IB - 2, after
+        // their last use for this one.
+        auto kb_copy = [&](int kb) __attribute__((always_inline)) {
+            return (PERSIST && has_next) ? (kb + 2 < IB ? kb + 2 : kb + 2 - IB) : min(kb + 2, IB - 1);
+        };
         auto copy_x = [&](int stage, int kb) __attribute__((always_inline)) {
-            if (PERSIST && has_next && kb + 2 >= IB) {
-                if (kb + 2 == IB) consts(buf ^ 1, en, row0n, nrowsn, ntn);
-                uint32_t o[C::B_LD];
+            if (PERSIST && has_next && kb + 2 == IB) {
+                consts(buf ^ 1, en, row0n, nrowsn, ntn);
 #pragma unroll
-                for (int i = 0; i < C::B_LD; ++i) o[i] = b_offset(i, en, ntn);
-                issue_b(stage, kb + 2 - IB, o);
-            } else {
-                issue_b(stage, min(kb + 2, IB - 1), b_off);
+                for (int i = 0; i < C::B_LD; ++i) b_off[i] = b_offset(i, en, ntn);
             }
+            issue_b(stage, kb_copy(kb), b_off);
         };
         auto copy_y = [&](int stage, int kb) __attribute__((always_inline)) {
-            if (PERSIST && has_next && kb + 2 >= IB) {
-                uint32_t o[C::A_LD];
+            if (PERSIST && has_next && kb + 2 == IB) {
 #pragma unroll
-                for (int i = 0; i < C::A_LD; ++i) o[i] = a_offset(i, row0n, nrowsn);
-                issue_a(stage, kb + 2 - IB, o);
-            } else {
-                issue_a(stage, min(kb + 2, IB - 1), a_off);
+                for (int i = 0; i < C::A_LD; ++i) a_off[i] = a_offset(i, row0n, nrowsn);
             }
+            issue_a(stage, kb_copy(kb), a_off);
         };
 
         if (wm * 64 >= nrows) {
@@ -482,22 +482,17 @@ __global__ __launch_bounds__(512) void gemm2_tile_w_kernel(Plan p, const uint8_t
             }
         }
         if (!PERSIST || !has_next) break;
-        t += t_step;
+        t += t_step;  // the copy offsets are the next tile's already
         e = en;
         row0 = row0n;
         nrows = nrowsn;
         nt = ntn;
         buf ^= 1;
-#pragma unroll
-        for (int i = 0; i < C::A_LD; ++i) a_off[i] = a_offset(i, row0, nrows);
-#pragma unroll
-        for (int i = 0; i < C::B_LD; ++i) b_off[i] = b_offset(i, e, nt);
     }
     wait_vmem();  // no copy into LDS may be pending when the workgroup ends
 }
 
-// Workgroups of the persistent variant: one per CU, a multiple of the 8 XCDs.
-static int persistent_grid() {
+int persistent_grid() {
     static std::atomic<int> cache[64];
     int dev = 0;
     if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) dev = 0;
