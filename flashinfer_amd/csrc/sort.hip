@@ -10,8 +10,9 @@
 //   * it also writes, per token, its slots in ascending local-expert order,
 //     which the combine kernel walks instead of scattering with atomics.
 //
-// Placement works per chunk of 1024 tokens (one per thread): each wave counts
-// its 64 tokens' hits per expert with one ballot per expert, the 16 wave
+// Placement works per chunk of tokens (one per thread: 1024 in the one-
+// workgroup sort, SORT_CHUNK_L in the two-pass sort for larger T): each wave
+// counts its 64 tokens' hits per expert with one ballot per expert, the wave
 // counts are scanned in LDS, and a lane's slot is chunk base + wave prefix +
 // popcount of the lower lanes' ballot bits.
 //
@@ -41,13 +42,14 @@ __device__ __forceinline__ void wave_counts(const TokLocal& tl, int lane, int wa
 
 // Places one chunk (every thread of the 1024-thread workgroup calls it).
 // base[e] holds the chunk's first slot for expert e.
+template <int CH>
 __device__ void place_chunk(const Plan& p, int t, bool valid, const TokLocal& tl, const int* base,
                             int (*wcnt)[EL], int tid, int lane, int wave) {
     wave_counts(tl, lane, wave, wcnt);
     __syncthreads();
     if (tid < EL) {
         int run = base[tid];
-        for (int w = 0; w < CHUNK / 64; ++w) {
+        for (int w = 0; w < CH / 64; ++w) {
             const int c = wcnt[w][tid];
             wcnt[w][tid] = run;
             run += c;
@@ -124,18 +126,18 @@ __global__ __launch_bounds__(1024) void route_sort_kernel(Plan p, const float* _
     sort_one_workgroup(p, s_ids, s_w, bm1, bm2, wcnt);
 }
 
-// Large T, pass 1: per-chunk expert totals into chunk_cnt[chunk][32].
-__global__ __launch_bounds__(1024) void sort_count_kernel(Plan p) {
-    __shared__ int wcnt[CHUNK / 64][EL];
+// Large T, pass 1: per-chunk (SORT_CHUNK_L tokens) expert totals into chunk_cnt[chunk][EL].
+__global__ __launch_bounds__(SORT_CHUNK_L) void sort_count_kernel(Plan p) {
+    __shared__ int wcnt[SORT_CHUNK_L / 64][EL];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int t = blockIdx.x * CHUNK + tid;
+    const int t = blockIdx.x * SORT_CHUNK_L + tid;
     const bool valid = t < p.T;
     const TokLocal tl = load_local(p.topk_ids, p.topk_w, t, valid, p.local_offset);
     wave_counts(tl, lane, wave, wcnt);
     __syncthreads();
     if (tid < EL) {
         int s = 0;
-        for (int w = 0; w < CHUNK / 64; ++w) s += wcnt[w][tid];
+        for (int w = 0; w < SORT_CHUNK_L / 64; ++w) s += wcnt[w][tid];
         p.chunk_cnt[blockIdx.x * EL + tid] = s;
     }
 }
@@ -143,15 +145,15 @@ __global__ __launch_bounds__(1024) void sort_count_kernel(Plan p) {
 // Large T, pass 2: each chunk derives its per-expert base from the chunk
 // totals (chunk 0 also writes the expert offsets and tile prefixes), then
 // places its tokens.
-__global__ __launch_bounds__(1024) void sort_place_kernel(Plan p, int nchunks, int bm1, int bm2) {
+__global__ __launch_bounds__(SORT_CHUNK_L) void sort_place_kernel(Plan p, int nchunks, int bm1, int bm2) {
     __shared__ int base[EL];
     __shared__ int s_before[EL], s_total[EL];
-    __shared__ int wcnt[CHUNK / 64][EL];
+    __shared__ int wcnt[SORT_CHUNK_L / 64][EL];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int cb = blockIdx.x;
     // The chunk's top-k rows are loaded first, so their round trip overlaps
     // the chunk totals'.
-    const int t = cb * CHUNK + tid;
+    const int t = cb * SORT_CHUNK_L + tid;
     const bool valid = t < p.T;
     const TokLocal tl = load_local(p.topk_ids, p.topk_w, t, valid, p.local_offset);
     // Chunk totals, every (chunk, expert) count loaded by its own thread (one
@@ -159,7 +161,7 @@ __global__ __launch_bounds__(1024) void sort_place_kernel(Plan p, int nchunks, i
     // (exact, so the order does not matter).
     if (tid < EL) { s_before[tid] = 0; s_total[tid] = 0; }
     __syncthreads();
-    for (int i = tid; i < nchunks * EL; i += CHUNK) {
+    for (int i = tid; i < nchunks * EL; i += SORT_CHUNK_L) {
         const int v = p.chunk_cnt[i];
         const int c = i / EL, e = i % EL;
         if (v) {
@@ -174,7 +176,7 @@ __global__ __launch_bounds__(1024) void sort_place_kernel(Plan p, int nchunks, i
         if (lane < EL) base[lane] = off + s_before[lane];
     }
     __syncthreads();
-    place_chunk(p, t, valid, tl, base, wcnt, tid, lane, wave);
+    place_chunk<SORT_CHUNK_L>(p, t, valid, tl, base, wcnt, tid, lane, wave);
 }
 
 bool route_sort_supported(int T) { return T > 0 && T <= ROUTE_SORT_MAX_T; }
@@ -218,14 +220,15 @@ hipError_t launch_sort(const Plan& p, int bm1, int bm2, hipStream_t s) {
         hipLaunchKernelGGL(sort_small_kernel, dim3(1), dim3(64), 0, s, p, bm1, bm2);
         return hipGetLastError();
     }
-    if (nchunks == 1) {
+    if (p.T <= CHUNK) {
         hipLaunchKernelGGL(sort_kernel, dim3(1), dim3(CHUNK), 0, s, p, bm1, bm2);
         return hipGetLastError();
     }
-    hipLaunchKernelGGL(sort_count_kernel, dim3(nchunks), dim3(CHUNK), 0, s, p);
+    hipLaunchKernelGGL(sort_count_kernel, dim3(nchunks), dim3(SORT_CHUNK_L), 0, s, p);
     hipError_t err = hipGetLastError();
     if (err != hipSuccess) return err;
-    hipLaunchKernelGGL(sort_place_kernel, dim3(nchunks), dim3(CHUNK), 0, s, p, nchunks, bm1, bm2);
+    hipLaunchKernelGGL(sort_place_kernel, dim3(nchunks), dim3(SORT_CHUNK_L), 0, s, p, nchunks, bm1,
+                       bm2);
     return hipGetLastError();
 }
 

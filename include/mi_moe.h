@@ -83,7 +83,7 @@ typedef struct mi_moe_args {
  *   sorted_tok int32 [kT]     token of each slot, expert-major, token-ascending
  *   sorted_w   fp32  [kT]     routing weight of each slot
  *   tok_slot   int32 [T, 8]   slots of each token, ascending local expert, -1 pad
- *   chunk_cnt  int32 [ceil(T/1024), E]  per-1024-token-chunk local expert counts
+ *   chunk_cnt  int32 [ceil(T/256), E]   per-256-token-chunk local expert counts
  *   act        bf16  [kT, 2048]  SwiGLU(GEMM1) per slot, rounded to bf16
  *   part       bf16  [kT, 7168]  routing weight x GEMM2 row per slot; fp32
  *                             (same offset, twice the bytes) at T <= 1024
